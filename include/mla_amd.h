@@ -1,0 +1,139 @@
+/*
+ * mla_amd.h -- C ABI of the MI355X (gfx950) MLA attention library
+ * (libmla_amd.so, built from mini-sglang_amd/csrc).
+ *
+ * Conventions
+ *   - Every entry point returns int: MLA_OK (0) on success, otherwise an
+ *     MLA_ERR_* code; mla_last_error() then returns a thread-local message.
+ *     This mirrors the reference's host::RuntimeCheck / PanicError, which
+ *     carry a file:line message (python/minisgl/kernel/csrc/include/minisgl/
+ *     utils.h:40-93) and surface as Python exceptions.
+ *   - Device buffers are plain pointers; strides are in ELEMENTS of the
+ *     buffer's own type unless the name says _bytes.
+ *   - `stream` is a hipStream_t (NULL = legacy default stream). No entry
+ *     point synchronises or allocates device memory, so every launch is
+ *     capturable into a HIP graph; the caller owns all buffers, including the
+ *     split-KV workspace, as the reference's backends own theirs
+ *     (python/minisgl/attention/fi.py:90-92).
+ *   - bf16 tensors are raw uint16 bit patterns (bfloat16).
+ */
+#ifndef MLA_AMD_H
+#define MLA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MLA_OK = 0,
+  MLA_ERR_INVALID_ARG = 1, /* shape, stride, alignment or range check failed */
+  MLA_ERR_HIP = 2,         /* a HIP runtime call failed (message has hipGetErrorString) */
+  MLA_ERR_UNSUPPORTED = 3  /* valid request outside what the kernels implement */
+};
+
+/* Latent KV row width of absorbed MLA: 512 latent (the value) + 64 rope. */
+#define MLA_KV_DIM 576
+#define MLA_V_DIM 512
+/* Decode work is planned in blocks of this many tokens. */
+#define MLA_PLAN_BLOCK 64
+/* Entries per CTA in a decode plan's cta_ranges and per request in req_info. */
+#define MLA_PLAN_CTA_INTS 4
+#define MLA_PLAN_REQ_INTS 3
+
+/* Message for the last failed call on this thread ("" if none). */
+const char *mla_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int mla_abi_version(void);
+
+/* Number of compute units of `device` (sizes decode plans). Host only. */
+int mla_device_cu_count(int device, int32_t *out);
+
+/*
+ * Row scatter: cache[indices[i]] = x[i] for i < num_rows, row_bytes each.
+ * Replaces StoreKernel<...>::run / store_kv_cache
+ * (python/minisgl/kernel/csrc/jit/store.cu:25-53,55-121) behind
+ * MHAKVCache.store_kv (python/minisgl/kvcache/mha_pool.py:45-56). Strides are
+ * in bytes; row_bytes and both strides must be multiples of 16 and the
+ * pointers 16-byte aligned. index_bits is 32 or 64. Indices must be distinct
+ * (the reference's own test relies on the same, tests/kernel/test_store.py:20);
+ * an index outside [0, cache_rows) is skipped rather than written.
+ */
+int mla_store_rows(void *cache, int64_t cache_rows, int64_t cache_row_stride_bytes,
+                   const void *x, int64_t x_row_stride_bytes, const void *indices,
+                   int32_t index_bits, int64_t num_rows, int64_t row_bytes, void *stream);
+
+/*
+ * Token table -> page table, bit-exact:
+ *   out[b, j] = token_table[table_idx[b], j * page_size] / page_size
+ * for j < ceil(max_seqlen_k / page_size). Replaces the slicing in
+ * FlashAttentionBackend.prepare_metadata (python/minisgl/attention/fa.py:92-97,
+ * identical in attention/trtllm.py:116-121). token_table rows are
+ * Context.page_table rows (python/minisgl/core.py:103-104); max_seqlen_k must
+ * not exceed token_table_cols, and a table_idx outside [0, token_table_rows)
+ * is clamped into range.
+ */
+int mla_page_table_from_tokens(const int32_t *token_table, int32_t token_table_rows,
+                               int32_t token_table_cols, int64_t token_table_stride,
+                               const int32_t *table_idx, int32_t batch, int32_t max_seqlen_k,
+                               int32_t page_size, int32_t *out, int64_t out_stride,
+                               void *stream);
+
+/*
+ * Split-KV decode plan (host only, no GPU needed). Balances the requests'
+ * MLA_PLAN_BLOCK-token blocks over `num_ctas` CTAs, each CTA taking one
+ * contiguous range of (request, block) space. Plays the role of FlashInfer's
+ * plan() in the reference's backend (python/minisgl/attention/fi.py:123-166).
+ *   cta_ranges[num_ctas*4] : {req_begin, blk_begin, req_end, blk_end} (end exclusive)
+ *   req_info[batch*3]      : {first_cta, num_pieces, slot_base}
+ *   *num_slots             : partial-result slots the plan needs in the workspace
+ * Pieces are at most max_piece_pages pages long.
+ */
+int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
+                    int32_t num_ctas, int32_t max_piece_pages, int32_t *cta_ranges,
+                    int32_t *req_info, int32_t *num_slots);
+
+/*
+ * Absorbed-MLA paged decode (one query token per request), bf16 in, fp32
+ * accumulate, bf16 out plus fp32 natural-log LSE. Replaces the attention call
+ * of BaseAttnBackend.forward (python/minisgl/attention/base.py:19-22;
+ * FA template python/minisgl/attention/fa.py:48-65) for MLA.
+ *   q        [batch, heads, 576]  strides (q_stride_b, q_stride_h), last dim contiguous
+ *   kv_pool  [num_pages, page_size, 576] latent cache, row stride kv_row_stride
+ *   page_table [batch, >= ceil(seq_len/page_size)] int32, row stride pt_stride
+ *   seq_lens [batch] int32 (device_len, includes the token being decoded)
+ *   plan     device copy of mla_decode_plan's cta_ranges followed by req_info
+ *   ws_o     [ws_slots, heads, 512] fp32, ws_lse [ws_slots, heads] fp32
+ *   out      [batch, heads, 512] strides (out_stride_b, out_stride_h)
+ *   lse      [batch, heads] fp32 (row stride lse_stride_b) or NULL
+ * heads is 16, 32, 48 or 64 (one wave per 16 heads); page_size a power of
+ * two; page ids outside [0, num_pages) are clamped into range.
+ * Launches the split kernel on num_ctas CTAs, then the LSE merge kernel.
+ */
+int mla_decode_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *kv_pool,
+                    int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
+                    const int32_t *page_table, int64_t pt_stride, const int32_t *seq_lens,
+                    int32_t batch, int32_t heads, float scale, const int32_t *plan,
+                    int32_t num_ctas, float *ws_o, float *ws_lse, int32_t ws_slots, void *out,
+                    int64_t out_stride_b, int64_t out_stride_h, float *lse, int64_t lse_stride_b,
+                    void *stream);
+
+/*
+ * fp32 log-sum-exp merge of split-KV partials (standalone form of the merge
+ * step of mla_decode_bf16). For request b with n = req_info[3b+1] pieces in
+ * slots s = req_info[3b+2] .. +n-1:
+ *   lse = ln sum_i exp(ws_lse[s_i]);  out = sum_i exp(ws_lse[s_i] - lse) * ws_o[s_i]
+ * n == 0 writes out = 0, lse = -inf.
+ */
+int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slots,
+                         const int32_t *req_info, int32_t batch, int32_t heads, void *out,
+                         int64_t out_stride_b, int64_t out_stride_h, float *lse,
+                         int64_t lse_stride_b, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLA_AMD_H */

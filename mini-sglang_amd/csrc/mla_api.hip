@@ -1,0 +1,329 @@
+// extern "C" entry points of libmla_amd.so (declared in include/mla_amd.h):
+// argument validation, the split-KV planner (host) and kernel launches.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <limits.h>
+
+#include <string>
+
+#include "../../include/mla_amd.h"
+#include "mla_common.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return MLA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(MLA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+
+// Fixed cost of one decode piece, in 64-token blocks of KV traffic: loading the
+// 64 heads' queries (73.7 KB) and writing/merging the partial output.
+constexpr int kPieceOverheadBlocks = 2;
+
+}  // namespace
+
+extern "C" {
+
+const char* mla_last_error(void) { return g_last_error.c_str(); }
+
+int mla_abi_version(void) { return 1; }
+
+int mla_device_cu_count(int device, int32_t* out) {
+  if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_status(e, "hipGetDeviceProperties");
+  *out = prop.multiProcessorCount;
+  return ok();
+}
+
+int mla_store_rows(void* cache, int64_t cache_rows, int64_t cache_row_stride_bytes, const void* x,
+                   int64_t x_row_stride_bytes, const void* indices, int32_t index_bits, int64_t num_rows,
+                   int64_t row_bytes, void* stream) {
+  if (num_rows < 0) return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: num_rows < 0");
+  if (num_rows == 0) return ok();
+  if (cache == nullptr || x == nullptr || indices == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: null pointer");
+  if (index_bits != 32 && index_bits != 64)
+    return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: index_bits must be 32 or 64, got %d", index_bits);
+  if (row_bytes <= 0 || row_bytes % 16 != 0)
+    return fail(MLA_ERR_UNSUPPORTED, "mla_store_rows: row_bytes %lld is not a positive multiple of 16",
+                (long long)row_bytes);
+  if (cache_row_stride_bytes < row_bytes || cache_row_stride_bytes % 16 != 0 || x_row_stride_bytes < row_bytes ||
+      x_row_stride_bytes % 16 != 0)
+    return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: strides must be multiples of 16 and >= row_bytes");
+  if (!aligned(cache, 16) || !aligned(x, 16))
+    return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: cache and x must be 16-byte aligned");
+  if (cache_rows <= 0) return fail(MLA_ERR_INVALID_ARG, "mla_store_rows: cache_rows must be positive");
+  return hip_status(mla::launch_store_rows(cache, cache_rows, cache_row_stride_bytes, x, x_row_stride_bytes,
+                                           indices, index_bits, num_rows, row_bytes, (hipStream_t)stream),
+                    "mla_store_rows launch");
+}
+
+int mla_page_table_from_tokens(const int32_t* token_table, int32_t token_table_rows, int32_t token_table_cols,
+                               int64_t token_table_stride, const int32_t* table_idx, int32_t batch,
+                               int32_t max_seqlen_k, int32_t page_size, int32_t* out, int64_t out_stride,
+                               void* stream) {
+  if (batch < 0 || max_seqlen_k < 0) return fail(MLA_ERR_INVALID_ARG, "mla_page_table_from_tokens: negative size");
+  if (page_size <= 0) return fail(MLA_ERR_INVALID_ARG, "mla_page_table_from_tokens: page_size must be positive");
+  const int32_t cols = (max_seqlen_k + page_size - 1) / page_size;
+  if (batch == 0 || cols == 0) return ok();
+  if (token_table == nullptr || table_idx == nullptr || out == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "mla_page_table_from_tokens: null pointer");
+  if (token_table_rows <= 0 || max_seqlen_k > token_table_cols || token_table_stride < token_table_cols)
+    return fail(MLA_ERR_INVALID_ARG,
+                "mla_page_table_from_tokens: max_seqlen_k %d exceeds the token table (%d x %d, stride %lld)",
+                max_seqlen_k, token_table_rows, token_table_cols, (long long)token_table_stride);
+  if (out_stride < cols)
+    return fail(MLA_ERR_INVALID_ARG, "mla_page_table_from_tokens: out_stride %lld < %d columns",
+                (long long)out_stride, cols);
+  return hip_status(mla::launch_page_table(token_table, token_table_rows, token_table_stride, table_idx, batch, cols,
+                                           page_size, out, out_stride, (hipStream_t)stream),
+                    "mla_page_table_from_tokens launch");
+}
+
+// Greedy contiguous partition of the requests' blocks with at most `cap`
+// cost units (blocks + kPieceOverheadBlocks per piece) per CTA and at most
+// max_blk blocks per piece. Returns the number of CTAs used, or INT32_MAX if a
+// CTA would overflow `limit` CTAs. Writes the plan when `write` is set.
+static int plan_greedy(const int32_t* seq_lens, int batch, int64_t cap, int64_t max_blk, int limit, bool write,
+                       int32_t* cta_ranges, int32_t* req_info, int32_t* num_slots) {
+  const int B = mla::kPlanBlock;
+  int w = 0;
+  int64_t used = 0;
+  int32_t slots = 0;
+  if (write) {
+    cta_ranges[0] = 0;
+    cta_ranges[1] = 0;
+  }
+  auto next_cta = [&](int b, int64_t blk) -> bool {
+    if (w + 1 >= limit) return false;
+    if (write) {
+      cta_ranges[4 * w + 2] = b;
+      cta_ranges[4 * w + 3] = (int32_t)blk;
+      cta_ranges[4 * (w + 1) + 0] = b;
+      cta_ranges[4 * (w + 1) + 1] = (int32_t)blk;
+    }
+    ++w;
+    used = 0;
+    return true;
+  };
+  for (int b = 0; b < batch; ++b) {
+    const int64_t nb = ((int64_t)seq_lens[b] + B - 1) / B;
+    int first = w, pieces = 0;
+    int64_t blk = 0;
+    while (blk < nb) {
+      const int64_t room = cap - used - kPieceOverheadBlocks;
+      if (room <= 0) {
+        if (used == 0) return INT32_MAX;  // cap too small for any block
+        if (!next_cta(b, blk)) return INT32_MAX;
+        continue;
+      }
+      int64_t take = nb - blk;
+      if (take > room) take = room;
+      if (take > max_blk) take = max_blk;
+      if (pieces == 0) first = w;
+      ++pieces;
+      blk += take;
+      used += take + kPieceOverheadBlocks;
+      if (blk < nb && !next_cta(b, blk)) return INT32_MAX;
+    }
+    if (write) {
+      req_info[3 * b + 0] = first;
+      req_info[3 * b + 1] = pieces;
+      req_info[3 * b + 2] = pieces >= 2 ? slots : 0;
+    }
+    if (pieces >= 2) slots += pieces;
+  }
+  if (write) {
+    cta_ranges[4 * w + 2] = batch;
+    cta_ranges[4 * w + 3] = 0;
+    for (int e = w + 1; e < limit; ++e) {
+      cta_ranges[4 * e + 0] = batch;
+      cta_ranges[4 * e + 1] = 0;
+      cta_ranges[4 * e + 2] = batch;
+      cta_ranges[4 * e + 3] = 0;
+    }
+    *num_slots = slots;
+  }
+  return w + 1;
+}
+
+int mla_decode_plan(const int32_t* seq_lens, int32_t batch, int32_t page_size, int32_t num_ctas,
+                    int32_t max_piece_pages, int32_t* cta_ranges, int32_t* req_info, int32_t* num_slots) {
+  if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: batch < 0");
+  if (num_ctas < 1) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: num_ctas must be >= 1");
+  if (!is_pow2(page_size)) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: page_size %d is not a power of two", page_size);
+  if (max_piece_pages < 1 || max_piece_pages > mla::kMaxPieceIds)
+    return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: max_piece_pages must be in [1, %d]", mla::kMaxPieceIds);
+  if (cta_ranges == nullptr || num_slots == nullptr || (batch > 0 && (seq_lens == nullptr || req_info == nullptr)))
+    return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: null pointer");
+  const int B = mla::kPlanBlock;
+  // Longest piece in blocks such that the pages it touches fit the LDS id buffer.
+  const int64_t max_blk = page_size <= B ? (int64_t)max_piece_pages * page_size / B
+                                         : (int64_t)(max_piece_pages - 1) * page_size / B;
+  if (max_blk < 1)
+    return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: max_piece_pages %d too small for page_size %d",
+                max_piece_pages, page_size);
+  int64_t total = 0;
+  for (int b = 0; b < batch; ++b) {
+    if (seq_lens[b] < 0) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: seq_lens[%d] < 0", b);
+    const int64_t nb = ((int64_t)seq_lens[b] + B - 1) / B;
+    total += nb + (nb > 0 ? kPieceOverheadBlocks : 0);
+  }
+  // Smallest per-CTA capacity for which the greedy partition fits num_ctas CTAs.
+  int64_t lo = kPieceOverheadBlocks + 1, hi = total + kPieceOverheadBlocks + 1;
+  if (plan_greedy(seq_lens, batch, hi, max_blk, num_ctas, false, nullptr, nullptr, nullptr) > num_ctas)
+    return fail(MLA_ERR_UNSUPPORTED,
+                "mla_decode_plan: %d CTAs cannot hold the batch with pieces of at most %lld blocks", num_ctas,
+                (long long)max_blk);
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (plan_greedy(seq_lens, batch, mid, max_blk, num_ctas, false, nullptr, nullptr, nullptr) <= num_ctas)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  plan_greedy(seq_lens, batch, lo, max_blk, num_ctas, true, cta_ranges, req_info, num_slots);
+  return ok();
+}
+
+static int check_out(const void* out, int64_t sb, int64_t sh, const float* lse, int64_t lse_sb, int32_t heads,
+                     const char* who) {
+  if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "%s: out is null", who);
+  if (!aligned(out, 16) || sb % 8 != 0 || sh % 8 != 0 || sh < 512 || sb < (int64_t)heads * sh)
+    return fail(MLA_ERR_INVALID_ARG,
+                "%s: out must be 16-byte aligned with strides (b=%lld, h=%lld) multiples of 8, h >= 512, "
+                "b >= heads*h",
+                who, (long long)sb, (long long)sh);
+  if (lse != nullptr && lse_sb < heads)
+    return fail(MLA_ERR_INVALID_ARG, "%s: lse row stride %lld < heads %d", who, (long long)lse_sb, heads);
+  return MLA_OK;
+}
+
+int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
+                    int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
+                    int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
+                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                    void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
+                    void* stream) {
+  const char* who = "mla_decode_bf16";
+  if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
+  if (batch == 0) return ok();
+  if (heads != 16 && heads != 32 && heads != 48 && heads != 64)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be 16, 32, 48 or 64, got %d", who, heads);
+  if (q == nullptr || kv_pool == nullptr || page_table == nullptr || seq_lens == nullptr || plan == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!aligned(q, 16) || q_stride_h % 8 != 0 || q_stride_b % 8 != 0 || q_stride_h < MLA_KV_DIM ||
+      q_stride_b < (int64_t)heads * q_stride_h)
+    return fail(MLA_ERR_INVALID_ARG, "%s: q must be 16-byte aligned, row-contiguous, strides multiples of 8", who);
+  if (!aligned(kv_pool, 16) || kv_row_stride % 8 != 0 || kv_row_stride < MLA_KV_DIM)
+    return fail(MLA_ERR_INVALID_ARG, "%s: kv_pool must be 16-byte aligned with row stride >= 576, multiple of 8",
+                who);
+  if (num_pages < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages must be >= 1", who);
+  if (!is_pow2(page_size)) return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d is not a power of two", who, page_size);
+  if (pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: pt_stride must be >= 1", who);
+  if (num_ctas < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_ctas must be >= 1", who);
+  if (!(scale > 0.f) || !isfinite(scale)) return fail(MLA_ERR_INVALID_ARG, "%s: scale must be finite and > 0", who);
+  if (ws_slots < 0 || (ws_slots > 0 && (ws_o == nullptr || ws_lse == nullptr)))
+    return fail(MLA_ERR_INVALID_ARG, "%s: workspace pointers are null", who);
+  if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
+  if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
+
+  mla::DecodeParams p;
+  p.q = static_cast<const __bf16*>(q);
+  p.q_stride_b = q_stride_b;
+  p.q_stride_h = q_stride_h;
+  p.kv = static_cast<const __bf16*>(kv_pool);
+  p.kv_row_stride = kv_row_stride;
+  p.num_pages = num_pages;
+  p.log2_ps = ilog2(page_size);
+  p.page_table = page_table;
+  p.pt_stride = pt_stride;
+  p.seq_lens = seq_lens;
+  p.batch = batch;
+  p.heads = heads;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.plan = plan;
+  p.num_ctas = num_ctas;
+  p.ws_o = ws_o;
+  p.ws_lse = ws_lse;
+  p.ws_slots = ws_slots;
+  p.out = static_cast<__bf16*>(out);
+  p.out_stride_b = out_stride_b;
+  p.out_stride_h = out_stride_h;
+  p.lse = lse;
+  p.lse_stride_b = lse_stride_b;
+  hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
+
+  mla::MergeParams m;
+  m.ws_o = ws_o;
+  m.ws_lse = ws_lse;
+  m.ws_slots = ws_slots;
+  m.req_info = plan + 4 * (int64_t)num_ctas;
+  m.batch = batch;
+  m.heads = heads;
+  m.skip_single = 1;
+  m.out = p.out;
+  m.out_stride_b = out_stride_b;
+  m.out_stride_h = out_stride_h;
+  m.lse = lse;
+  m.lse_stride_b = lse_stride_b;
+  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch");
+}
+
+int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
+                         int32_t batch, int32_t heads, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                         float* lse, int64_t lse_stride_b, void* stream) {
+  const char* who = "mla_decode_merge_f32";
+  if (batch < 0 || heads < 1 || ws_slots < 0) return fail(MLA_ERR_INVALID_ARG, "%s: invalid sizes", who);
+  if (batch == 0) return ok();
+  if (req_info == nullptr || (ws_slots > 0 && (ws_o == nullptr || ws_lse == nullptr)))
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
+  if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
+  mla::MergeParams m;
+  m.ws_o = ws_o;
+  m.ws_lse = ws_lse;
+  m.ws_slots = ws_slots;
+  m.req_info = req_info;
+  m.batch = batch;
+  m.heads = heads;
+  m.skip_single = 0;
+  m.out = static_cast<__bf16*>(out);
+  m.out_stride_b = out_stride_b;
+  m.out_stride_h = out_stride_h;
+  m.lse = lse;
+  m.lse_stride_b = lse_stride_b;
+  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_merge_f32 launch");
+}
+
+}  // extern "C"

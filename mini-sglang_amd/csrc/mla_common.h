@@ -1,0 +1,76 @@
+// Shared types and constants of the gfx950 MLA kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mla {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
+typedef __bf16 bf16x4 __attribute__((__vector_size__(8)));
+typedef float f32x4 __attribute__((__vector_size__(16)));
+typedef float f32x16 __attribute__((__vector_size__(64)));
+typedef uint32_t u32x4 __attribute__((__vector_size__(16)));
+typedef uint32_t u32x2 __attribute__((__vector_size__(8)));
+
+#define MLA_LDS __attribute__((address_space(3)))
+
+// Absorbed-MLA latent row: 512 latent dims (also the value) + 64 rope dims, bf16.
+constexpr int kKvDim = 576;
+constexpr int kVDim = 512;
+constexpr int kRowBytes = kKvDim * 2;  // 1152
+constexpr int kRowChunks = kRowBytes / 16;  // 72 16-byte chunks per row
+// Decode LDS tile: 32 tokens, staged by wave-wide 16-byte DMA loads (1 KiB each).
+constexpr int kTile = 32;
+constexpr int kTileBytes = kTile * kRowBytes;  // 36864
+constexpr int kTileDma = kTileBytes / 1024;    // 36 wave-wide DMA loads per tile
+constexpr int kStages = 4;                     // LDS ring depth (147456 bytes)
+constexpr int kPlanBlock = 64;                 // tokens per plan block
+constexpr int kMaxPieceIds = 1024;             // page ids of one piece staged in LDS
+
+struct DecodeParams {
+  const __bf16* q;  // [B, H, 576]
+  int64_t q_stride_b, q_stride_h;
+  const __bf16* kv;  // [pages * ps, 576] rows
+  int64_t kv_row_stride;  // elements
+  int32_t num_pages;
+  int32_t log2_ps;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  const int32_t* seq_lens;
+  int32_t batch, heads;
+  float scale_log2;  // softmax scale * log2(e)
+  const int32_t* plan;  // [num_ctas * 4] ranges, then [batch * 3] request info
+  int32_t num_ctas;
+  float* ws_o;    // [ws_slots, H, 512]
+  float* ws_lse;  // [ws_slots, H]
+  int32_t ws_slots;
+  __bf16* out;  // [B, H, 512]
+  int64_t out_stride_b, out_stride_h;
+  float* lse;  // [B, H] or null
+  int64_t lse_stride_b;
+};
+
+struct MergeParams {
+  const float* ws_o;
+  const float* ws_lse;
+  int32_t ws_slots;
+  const int32_t* req_info;  // [batch * 3]
+  int32_t batch, heads;
+  int32_t skip_single;  // requests with one piece were finalised by the decode kernel
+  __bf16* out;
+  int64_t out_stride_b, out_stride_h;
+  float* lse;
+  int64_t lse_stride_b;
+};
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
+hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
+                             const void* indices, int index_bits, int64_t rows, int64_t row_bytes,
+                             hipStream_t stream);
+hipError_t launch_page_table(const int32_t* tt, int32_t tt_rows, int64_t tt_stride, const int32_t* table_idx,
+                             int32_t batch, int32_t cols, int32_t page_size, int32_t* out,
+                             int64_t out_stride, hipStream_t stream);
+
+}  // namespace mla

@@ -1,0 +1,387 @@
+// Absorbed-MLA paged decode for gfx950 (MI355X), split-KV, plus the fp32
+// log-sum-exp merge of the split partials.
+//
+// Work decomposition: a CTA (one wave per 16 query heads) owns one contiguous
+// range of (request, 64-token block) space from the host plan. For each piece
+// of a request in its range it streams the piece's latent KV rows through a
+// 4-stage LDS ring (wave-wide 16-byte global->LDS DMA loads, no register
+// staging) and every wave reuses each staged row for its 16 heads:
+//   S^T[32 tok x 16 heads] = K[32 x 576] . Q^T    (bf16 MFMA 16x16x32, K from LDS, Q in VGPRs)
+//   O^T[512 x 16 heads]   += V^T[512 x 32] . P^T   (V^T read with ds_read_b64_tr_b16)
+// with an online softmax in the log2 domain between them. A piece that covers
+// its whole request writes bf16 output directly; a partial piece writes its
+// normalised fp32 output and natural-log LSE to a workspace slot that the
+// merge kernel folds together.
+//
+// LDS row layout: token t's 72 16-byte chunks are stored XOR-swizzled,
+// chunk c at position c ^ swz(t & 7), so both the 16-byte K reads (8
+// consecutive tokens, same chunk) and the transposing V reads (4 consecutive
+// tokens, two adjacent chunks) hit 32 distinct banks.
+//
+// MFMA 16x16x32 bf16 lane layout (wave64, lane l, g = l/16, c = l%16):
+//   A[m][k]: m = c, k = 8g + j (j = 0..7);  B[k][n]: n = c, k = 8g + j
+//   D[m][n]: n = c, m = 4g + i (i = 0..3)
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j%4
+// of the 8-byte words addressed by lanes j/4 + 4k, k = 0..3.
+#include "mla_common.h"
+
+namespace mla {
+namespace {
+
+__device__ __forceinline__ int swz(int t7) { return ((t7 & 3) << 1) | ((t7 >> 2) & 1); }
+
+__device__ __forceinline__ float wave_max_g(float v) {
+  // reduce over the 4 lane groups (lanes l, l^16, l^32, l^48)
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_g(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+// The counter saturates at 63; a smaller count only waits longer, so N is clamped.
+template <int N0>
+__device__ __forceinline__ void wait_vmcnt() {
+  constexpr int N = N0 > 63 ? 63 : N0;
+  static_assert(N >= 0, "vmcnt range");
+  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4]=7 | lgkmcnt[11:8]=15 | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+
+// 16-byte global -> LDS DMA; lane i's data lands at LDS byte address
+// lds_base + 16*i. Issued as inline asm so that the compiler's wait-count
+// pass does not serialise later LDS reads of other stages behind it: every
+// read of a staged tile is preceded by wait_vmcnt + a workgroup barrier.
+__device__ __forceinline__ void dma16_saddr(const char* base, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  // round-to-nearest-even, matching torch's float->bfloat16 conversion
+  __bf16 x = (__bf16)a, y = (__bf16)b;
+  uint16_t ux = __builtin_bit_cast(uint16_t, x), uy = __builtin_bit_cast(uint16_t, y);
+  return (uint32_t)ux | ((uint32_t)uy << 16);
+}
+
+// Softmax rescaling is skipped until a head's running max grows by more than
+// this many log2 units; exp2 of a stale-max score then stays below 2^8.
+constexpr float kRescaleLog2 = 8.0f;
+constexpr int kKPrefetch = 8;  // K operands (16-byte LDS reads) in flight
+constexpr int kVPrefetch = 4;  // V operand pairs (transposing LDS reads) in flight
+
+template <int NW, bool kPageCoversTile>
+__global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodeParams p) {
+  constexpr int kDmaPerWave = kTileDma / NW;
+  static_assert(kTileDma % NW == 0, "tile DMA split");
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * kTileBytes];
+  __shared__ int s_ids[kMaxPieceIds];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int w = blockIdx.x;
+
+  const int32_t* cta = p.plan + 4 * w;
+  const int rb = cta[0], kb = cta[1], re = cta[2], ke = cta[3];
+  const int32_t* req_info = p.plan + 4 * p.num_ctas;
+  const int ps_mask = (1 << p.log2_ps) - 1;
+  const int row_bytes = (int)(p.kv_row_stride * 2);
+  const char* kv = reinterpret_cast<const char*>(p.kv);
+  const uint32_t lds_ring = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
+
+  // per-lane LDS read offsets (bytes within a tile)
+  const int xk = swz(c & 7);
+  const int k_off_even = c * kRowBytes + ((g ^ xk) << 4);
+  const int k_off_odd = c * kRowBytes + (((4 + g) ^ xk) << 4);
+  const int v_row = (4 * g + (c >> 2)) * kRowBytes;
+  int v_off[4];
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    v_off[q4] = v_row + ((2 * (q4 ^ (c >> 2)) + (((c & 3) >> 1) ^ (g & 1))) << 4) + ((c & 1) << 3);
+
+  // per-lane DMA slot of each of this wave's loads: token t_k, swizzled chunk byte offset
+  int dma_t[kDmaPerWave], dma_c16[kDmaPerWave];
+#pragma unroll
+  for (int k = 0; k < kDmaPerWave; ++k) {
+    const int s = (wave + k * NW) * 64 + lane;
+    const int t = (s * 7282) >> 19;  // s / 72 for s < 2304
+    dma_t[k] = t;
+    dma_c16[k] = ((s - t * kRowChunks) ^ swz(t & 7)) << 4;
+  }
+
+  for (int b = rb; b <= re && b < p.batch; ++b) {
+    const int L = p.seq_lens[b];
+    const int t0 = (b == rb) ? kb * kPlanBlock : 0;
+    const int t1 = (b == re) ? min(ke * kPlanBlock, L) : L;
+    if (t1 <= t0) continue;
+    const int first_cta = req_info[3 * b];
+    const int npieces = req_info[3 * b + 1];
+    const int slot_base = req_info[3 * b + 2];
+
+    // ---- Q^T operand (B of the QK MFMA): head c of this wave, dims ks*32 + 8g .. +8
+    const int h = wave * 16 + c;
+    const __bf16* qrow = p.q + (int64_t)b * p.q_stride_b + (int64_t)h * p.q_stride_h + g * 8;
+    bf16x8 qf[18];
+#pragma unroll
+    for (int ks = 0; ks < 18; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
+
+    // ---- page ids of the piece -> LDS
+    const int pg0 = t0 >> p.log2_ps;
+    const int npg = ((t1 - 1) >> p.log2_ps) - pg0 + 1;
+    __syncthreads();  // previous piece is done with s_ids and the ring
+    const int32_t* pt_row = p.page_table + (int64_t)b * p.pt_stride + pg0;
+    for (int i = threadIdx.x; i < npg && i < kMaxPieceIds; i += NW * 64) {
+      const int id = pt_row[i];
+      s_ids[i] = min(max(id, 0), p.num_pages - 1);
+    }
+    __syncthreads();
+
+    const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+
+    auto issue = [&](int tile, int stage) {
+      const int tstart = t0 + tile * kTile;
+      const int tlim = t1 - 1 - tstart;  // last valid token of the tile (loads clamp to it)
+      const uint32_t lds_stage = lds_ring + stage * kTileBytes;
+      if constexpr (kPageCoversTile) {
+        const int pid = __builtin_amdgcn_readfirstlane(s_ids[(tstart >> p.log2_ps) - pg0]);
+        const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (tstart & ps_mask)) * row_bytes;
+        if (tlim >= kTile - 1) {
+#pragma unroll
+          for (int k = 0; k < kDmaPerWave; ++k)
+            dma16_saddr(tsrc, dma_t[k] * row_bytes + dma_c16[k], lds_stage + (wave + k * NW) * 1024);
+        } else {
+#pragma unroll
+          for (int k = 0; k < kDmaPerWave; ++k)
+            dma16_saddr(tsrc, min(dma_t[k], tlim) * row_bytes + dma_c16[k], lds_stage + (wave + k * NW) * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < kDmaPerWave; ++k) {
+          const int tok = tstart + min(dma_t[k], tlim);
+          const int pid = s_ids[(tok >> p.log2_ps) - pg0];
+          const char* src = kv + ((int64_t)pid * (ps_mask + 1) + (tok & ps_mask)) * row_bytes + dma_c16[k];
+          dma16_vaddr(src, lds_stage + (wave + k * NW) * 1024);
+        }
+      }
+    };
+
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < ntiles) issue(s, s);
+
+    f32x4 O[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    for (int it = 0; it < ntiles; ++it) {
+      const int ahead = ntiles - 1 - it;  // tiles issued after this one (capped below)
+      if (ahead >= kStages - 2) wait_vmcnt<kDmaPerWave * (kStages - 2)>();
+      else if (ahead == 1) wait_vmcnt<kDmaPerWave>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+      if (it + kStages - 1 < ntiles) issue(it + kStages - 1, (it + kStages - 1) % kStages);
+
+      const MLA_LDS char* T = (const MLA_LDS char*)smem + (it % kStages) * kTileBytes;
+
+      // ---- S^T = K . Q^T : tokens 0-15 (s0) and 16-31 (s1) of the tile.
+      // Read j covers k-step j>>1 of token block j&1.
+      auto kread = [&](int j) {
+        const int ks = j >> 1;
+        const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (j & 1) * 16 * kRowBytes;
+        return *reinterpret_cast<const MLA_LDS bf16x8*>(T + off);
+      };
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      bf16x8 kbuf[kKPrefetch];
+#pragma unroll
+      for (int j = 0; j < kKPrefetch; ++j) kbuf[j] = kread(j);
+#pragma unroll
+      for (int j = 0; j < 36; ++j) {
+        const bf16x8 a = kbuf[j % kKPrefetch];
+        if (j + kKPrefetch < 36) kbuf[j % kKPrefetch] = kread(j + kKPrefetch);
+        if (j & 1) s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j >> 1], s1, 0, 0, 0);
+        else s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j >> 1], s0, 0, 0, 0);
+      }
+
+      // V^T operands do not depend on P: start reading them before the softmax.
+      auto vread = [&](int db, int half) {
+        const int off = v_off[db & 3] + 128 * (db >> 2) + half * 16 * kRowBytes;
+        return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(T + off));
+      };
+      bf16x4 vlo[kVPrefetch], vhi[kVPrefetch];
+#pragma unroll
+      for (int j = 0; j < kVPrefetch; ++j) {
+        vlo[j] = vread(j, 0);
+        vhi[j] = vread(j, 1);
+      }
+
+      // ---- online softmax (log2 domain) for head c; lane holds tokens 4g+i and 16+4g+i
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = s0[i] * p.scale_log2;
+        x[4 + i] = s1[i] * p.scale_log2;
+      }
+      const int tstart = t0 + it * kTile;
+      if (tstart + kTile > t1) {
+        const int valid = t1 - tstart;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (4 * g + i >= valid) x[i] = -INFINITY;
+          if (16 + 4 * g + i >= valid) x[4 + i] = -INFINITY;
+        }
+      }
+      float mt = x[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mt = fmaxf(mt, x[i]);
+      mt = wave_max_g(mt);
+      if (it == 0) {
+        m_run = mt;  // O and l are still zero
+      } else if (__any(mt > m_run + kRescaleLog2)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 32; ++db) O[db] = O[db] * alpha;
+        m_run = m_new;
+      }
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
+        l_run += pr[i];
+      }
+      u32x4 pw;
+      pw[0] = pack_bf16x2(pr[0], pr[1]);
+      pw[1] = pack_bf16x2(pr[2], pr[3]);
+      pw[2] = pack_bf16x2(pr[4], pr[5]);
+      pw[3] = pack_bf16x2(pr[6], pr[7]);
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+
+      // ---- O^T += V^T . P^T over 32 blocks of 16 dims
+#pragma unroll
+      for (int db = 0; db < 32; ++db) {
+        const bf16x8 a =
+            __builtin_shufflevector(vlo[db % kVPrefetch], vhi[db % kVPrefetch], 0, 1, 2, 3, 4, 5, 6, 7);
+        if (db + kVPrefetch < 32) {
+          vlo[db % kVPrefetch] = vread(db + kVPrefetch, 0);
+          vhi[db % kVPrefetch] = vread(db + kVPrefetch, 1);
+        }
+        O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, O[db], 0, 0, 0);
+      }
+    }
+
+    // ---- finalise: lane holds head h, dims 16*db + 4g + (0..3)
+    const float l_tot = wave_sum_g(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float lse_nat = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    if (npieces == 1) {
+      __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 4 * g;
+#pragma unroll
+      for (int db = 0; db < 32; ++db) {
+        u32x2 v;
+        v[0] = pack_bf16x2(O[db][0] * inv, O[db][1] * inv);
+        v[1] = pack_bf16x2(O[db][2] * inv, O[db][3] * inv);
+        *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+      }
+      if (p.lse != nullptr && g == 0) p.lse[(int64_t)b * p.lse_stride_b + h] = lse_nat;
+    } else {
+      const int slot = slot_base + (w - first_cta);
+      if (slot >= 0 && slot < p.ws_slots) {
+        float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 32; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[db] * inv;
+        if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
+      }
+    }
+  }
+}
+
+// One wave per (request, head): lane holds dims 8*lane .. +8.
+__global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (h >= p.heads) return;
+  const int n = p.req_info[3 * b + 1];
+  const int base = p.req_info[3 * b + 2];
+  if (n == 1 && p.skip_single) return;
+  __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 8 * lane;
+
+  float mx = -INFINITY;
+  for (int i = lane; i < n; i += 64) {
+    const int s = base + i;
+    if (s >= 0 && s < p.ws_slots) mx = fmaxf(mx, p.ws_lse[(int64_t)s * p.heads + h]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+  if (mx > -INFINITY) {
+    for (int i = lane; i < n; i += 64) {
+      const int s = base + i;
+      if (s >= 0 && s < p.ws_slots) sum += expf(p.ws_lse[(int64_t)s * p.heads + h] - mx);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+  const bool any = mx > -INFINITY && sum > 0.f;
+  const float lse = any ? mx + logf(sum) : -INFINITY;
+
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (any) {
+    for (int i = 0; i < n; ++i) {
+      const int s = base + i;
+      if (s < 0 || s >= p.ws_slots) continue;
+      const float wgt = expf(p.ws_lse[(int64_t)s * p.heads + h] - lse);
+      const f32x4* src = reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
+      const f32x4 a = src[0], bq = src[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] += wgt * a[j];
+        acc[4 + j] += wgt * bq[j];
+      }
+    }
+  }
+  u32x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = pack_bf16x2(acc[2 * j], acc[2 * j + 1]);
+  *reinterpret_cast<u32x4*>(orow) = v;
+  if (p.lse != nullptr && lane == 0) p.lse[(int64_t)b * p.lse_stride_b + h] = lse;
+}
+
+template <int NW>
+hipError_t launch_decode_nw(const DecodeParams& p, hipStream_t stream) {
+  if (p.log2_ps >= 5)
+    hipLaunchKernelGGL((mla_decode_kernel<NW, true>), dim3(p.num_ctas), dim3(NW * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((mla_decode_kernel<NW, false>), dim3(p.num_ctas), dim3(NW * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  switch (p.heads / 16) {
+    case 1: return launch_decode_nw<1>(p, stream);
+    case 2: return launch_decode_nw<2>(p, stream);
+    case 3: return launch_decode_nw<3>(p, stream);
+    case 4: return launch_decode_nw<4>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_merge(const MergeParams& p, hipStream_t stream) {
+  dim3 grid(p.batch, (p.heads + 3) / 4);
+  hipLaunchKernelGGL(mla_merge_kernel, grid, dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace mla

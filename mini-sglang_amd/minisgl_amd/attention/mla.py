@@ -1,0 +1,204 @@
+"""MI355X MLA attention backend (absorbed decode + chunked prefill).
+
+Implements the five methods of ``BaseAttnBackend``
+(python/minisgl/attention/base.py:18-34) following the FlashAttention
+backend's metadata and capture flow (python/minisgl/attention/fa.py:36-136),
+with the attention math in libmla_amd.so:
+
+* ``prepare_metadata`` builds, from ``batch.padded_reqs``, the per-request
+  lengths (fa.py:71-90), the page table (fa.py:92-97, by a bit-exact HIP
+  gather kernel) and -- for decode -- a split-KV plan computed on the host by
+  the library's planner (the role FlashInfer's plan() plays in fi.py:123-166).
+  Host arrays go to the device with pinned non-blocking copies (fa.py:76-90).
+* ``forward`` stores the new latent rows into the pool (fa.py:53) and runs the
+  absorbed decode kernel: ``q [B, H, 576]`` -> ``o [B, H, 512]`` (latent
+  space; the caller applies W_UV).
+* the capture hooks point the metadata at static buffers sized for the
+  largest captured batch (fa.py:107-136); replay copies the live metadata in.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List
+
+import numpy as np
+import torch
+
+from ..config import MLAConfig
+from ..core import Batch, get_global_ctx
+from ..kernel import lib
+from ..kvcache.mla_pool import MLAKVCache
+from .base import BaseAttnBackend, BaseAttnMetadata
+from .utils import BaseCaptureData
+
+_CPU_I32 = {"device": "cpu", "dtype": torch.int32, "pin_memory": True}
+
+
+@dataclass
+class MLACaptureData(BaseCaptureData):
+    plan: torch.Tensor  # int32 [num_ctas * 4 + max_bs * 3]
+
+
+@dataclass
+class MLAMetadata(BaseAttnMetadata):
+    cu_seqlens_k: torch.Tensor
+    cu_seqlens_q: torch.Tensor
+    cache_seqlens: torch.Tensor  # int32 [bs] device_len per request
+    max_seqlen_k: int
+    max_seqlen_q: int
+    page_table: torch.Tensor  # int32 [bs, ceil(max_seqlen_k / ps)] page ids
+    is_decode: bool
+    plan: torch.Tensor | None = None  # decode split-KV plan (device)
+    num_slots: int = 0
+
+    def get_last_indices(self, bs: int) -> torch.Tensor:
+        return self.cu_seqlens_q[1 : 1 + bs] - 1
+
+
+class MLAAttnBackend(BaseAttnBackend):
+    def __init__(self, config: MLAConfig, num_ctas: int | None = None):
+        ctx = get_global_ctx()
+        assert isinstance(ctx.kv_cache, MLAKVCache), "the MLA backend needs an MLAKVCache pool"
+        self.config = config
+        self.kvcache: MLAKVCache = ctx.kv_cache
+        self.page_size = ctx.page_size
+        self.device = self.kvcache.device
+        self.scale = config.softmax_scale
+        self.num_heads = config.num_heads
+        dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        # one persistent decode CTA per compute unit
+        self.num_ctas = num_ctas or lib.device_cu_count(dev_index)
+        self.capture: MLACaptureData | None = None
+        self.capture_bs: List[int] = []
+        self.max_graph_bs = 0
+        self.ws_o: torch.Tensor | None = None
+        self.ws_lse: torch.Tensor | None = None
+        self.last_lse: torch.Tensor | None = None  # natural-log LSE of the last forward
+
+    # ------------------------------------------------------------------ workspace
+    def _ensure_workspace(self, slots: int) -> None:
+        have = 0 if self.ws_o is None else self.ws_o.shape[0]
+        if slots <= have:
+            return
+        assert self.capture is None, "captured graphs hold the workspace: it is sized once in init_capture_graph"
+        assert not torch.cuda.is_current_stream_capturing(), "workspace must be sized before capture"
+        self.ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.float32, device=self.device)
+        self.ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_id: int, batch: Batch) -> torch.Tensor:
+        metadata = batch.attn_metadata
+        assert isinstance(metadata, MLAMetadata)
+        self.kvcache.store_kv(k, v, batch.out_loc, layer_id)
+        if not metadata.is_decode:
+            raise NotImplementedError("MLA chunked prefill is not available in this build of libmla_amd")
+        B, H, _ = q.shape
+        out = torch.empty((B, H, self.config.kv_lora_rank), dtype=q.dtype, device=q.device)
+        lse = torch.empty((B, H), dtype=torch.float32, device=q.device)
+        lib.mla_decode(
+            q, self.kvcache.latent_cache(layer_id), metadata.page_table, metadata.cache_seqlens, metadata.plan,
+            self.num_ctas, self.ws_o, self.ws_lse, self.scale, out, lse,
+        )
+        self.last_lse = lse
+        return out
+
+    # ------------------------------------------------------------------ metadata
+    def prepare_metadata(self, batch: Batch) -> None:
+        reqs = batch.padded_reqs
+        padded_size = len(reqs)
+        seqlens_q = [r.extend_len for r in reqs]
+        seqlens_k = [r.device_len for r in reqs]
+        cached_lens = [r.cached_len for r in reqs]
+        max_seqlen_k = max(seqlens_k)
+        max_seqlen_q = max(seqlens_q)
+        device = self.device
+
+        cache_seqlens = torch.tensor(seqlens_k, **_CPU_I32).to(device, non_blocking=True)
+        cu_seqlens_k = torch.tensor([0] + seqlens_k, **_CPU_I32).cumsum_(dim=0).to(device, non_blocking=True)
+        if max_seqlen_q == 1:
+            cu_seqlens_q = torch.arange(0, padded_size + 1, device=device, dtype=torch.int32)
+        elif all(c == 0 for c in cached_lens):  # prefill with no cache hit
+            cu_seqlens_q = cu_seqlens_k
+        else:
+            cu_seqlens_q = torch.tensor([0] + seqlens_q, **_CPU_I32).cumsum_(dim=0).to(device, non_blocking=True)
+
+        table_idx = torch.tensor([r.table_idx for r in reqs], **_CPU_I32).to(device, non_blocking=True)
+        page_table = lib.page_table_from_tokens(get_global_ctx().page_table, table_idx, max_seqlen_k, self.page_size)
+
+        is_decode = batch.is_decode
+        plan_dev, slots = None, 0
+        if is_decode:
+            assert max_seqlen_q == 1, "decode batches extend every request by one token"
+            plan_np, slots = lib.decode_plan(seqlens_k, self.page_size, self.num_ctas)
+            self._ensure_workspace(max(slots, 1))
+            plan_dev = torch.from_numpy(plan_np).pin_memory().to(device, non_blocking=True)
+        batch.attn_metadata = MLAMetadata(
+            cu_seqlens_k=cu_seqlens_k,
+            cu_seqlens_q=cu_seqlens_q,
+            cache_seqlens=cache_seqlens,
+            max_seqlen_k=max_seqlen_k,
+            max_seqlen_q=max_seqlen_q,
+            page_table=page_table,
+            is_decode=is_decode,
+            plan=plan_dev,
+            num_slots=slots,
+        )
+
+    # ------------------------------------------------------------------ graph capture
+    def init_capture_graph(self, max_seq_len: int, bs_list: List[int]) -> None:
+        assert self.capture is None, "Capture already initialized."
+        max_bs = max(bs_list)
+        cols = -(-max_seq_len // self.page_size)
+        plan = torch.zeros((self.num_ctas * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS,), dtype=torch.int32,
+                           device=self.device)
+        # a plan never needs more partial slots than CTAs plus requests
+        self._ensure_workspace(self.num_ctas + max_bs)
+        self.capture = MLACaptureData.create(max_bs, cols, self.device, plan=plan)
+        self.max_graph_bs = max_bs
+        self.capture_bs = sorted(bs_list)
+
+    def prepare_for_capture(self, batch: Batch) -> None:
+        assert (bs := batch.size) in self.capture_bs and self.capture is not None
+        cap = self.capture
+        plan_np, _ = lib.decode_plan([r.device_len for r in batch.reqs], self.page_size, self.num_ctas)
+        n = plan_np.shape[0]
+        cap.plan[:n].copy_(torch.from_numpy(plan_np))
+        batch.attn_metadata = MLAMetadata(
+            cu_seqlens_k=cap.cu_seqlens_k[: bs + 1],
+            cu_seqlens_q=cap.cu_seqlens_q[: bs + 1],
+            cache_seqlens=cap.seq_lens[:bs],
+            max_seqlen_k=cap.page_table.size(1) * self.page_size,
+            max_seqlen_q=1,
+            page_table=cap.page_table[:bs, :],
+            is_decode=True,
+            plan=cap.plan,
+            num_slots=self.ws_o.shape[0],
+        )
+
+    def prepare_for_replay(self, batch: Batch) -> None:
+        metadata, bs = batch.attn_metadata, batch.padded_size
+        assert isinstance(metadata, MLAMetadata) and metadata.is_decode
+        assert self.capture is not None and bs in self.capture_bs
+        cap = self.capture
+        table_len = metadata.page_table.size(1)
+        cap.cu_seqlens_k[: bs + 1].copy_(metadata.cu_seqlens_k)
+        cap.seq_lens[:bs].copy_(metadata.cache_seqlens)
+        cap.page_table[:bs, :table_len].copy_(metadata.page_table)
+        cap.plan[: metadata.plan.numel()].copy_(metadata.plan)
+
+
+def plan_pieces(plan: np.ndarray, num_ctas: int, seq_lens) -> List[tuple]:
+    """Decode a host plan into ``(cta, request, t0, t1)`` pieces (for tests and tools)."""
+    B = len(seq_lens)
+    cta = plan[: num_ctas * lib.PLAN_CTA_INTS].reshape(num_ctas, 4)
+    out = []
+    for w in range(num_ctas):
+        rb, kb, re, ke = (int(x) for x in cta[w])
+        for b in range(rb, min(re, B - 1) + 1):
+            L = int(seq_lens[b])
+            t0 = kb * lib.PLAN_BLOCK if b == rb else 0
+            t1 = min(ke * lib.PLAN_BLOCK, L) if b == re else L
+            if t1 > t0:
+                out.append((w, b, t0, t1))
+    return out

@@ -1,0 +1,200 @@
+"""ctypes binding of libmla_amd.so (C ABI declared in include/mla_amd.h).
+
+The library is required: every entry here raises if it is missing or a call
+fails, mirroring the reference's RuntimeCheck -> Python exception path
+(python/minisgl/kernel/csrc/include/minisgl/utils.h:40-93). There is no
+fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+from typing import Tuple
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmla_amd.so")
+
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+# symbol -> (restype, argtypes); must match include/mla_amd.h
+SIGNATURES = {
+    "mla_last_error": (ctypes.c_char_p, []),
+    "mla_abi_version": (ctypes.c_int, []),
+    "mla_device_cu_count": (ctypes.c_int, [ctypes.c_int, _c_i32p]),
+    "mla_store_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp]),
+    "mla_page_table_from_tokens": (
+        ctypes.c_int,
+        [_vp, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "mla_decode_plan": (ctypes.c_int, [_c_i32p, _i32, _i32, _i32, _i32, _c_i32p, _c_i32p, _c_i32p]),
+    "mla_decode_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i32,
+         _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
+    "mla_decode_merge_f32": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _vp]),
+}
+
+ABI_VERSION = 1
+PLAN_BLOCK = 64
+PLAN_CTA_INTS = 4
+PLAN_REQ_INTS = 3
+MAX_PIECE_PAGES = 1024
+
+
+class MLAKernelError(RuntimeError):
+    """A libmla_amd entry point returned an error code."""
+
+
+@functools.lru_cache(maxsize=None)
+def load_library() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise MLAKernelError(
+            f"{LIB_PATH} is missing: build it with `python mini-sglang_amd/build.py` "
+            "(the MLA backend has no non-HIP fallback)"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.mla_abi_version() != ABI_VERSION:
+        raise MLAKernelError(f"libmla_amd ABI {lib.mla_abi_version()} != expected {ABI_VERSION}")
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().mla_last_error().decode(errors="replace")
+        raise MLAKernelError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def device_cu_count(device: int = 0) -> int:
+    out = ctypes.c_int32(0)
+    check(load_library().mla_device_cu_count(device, ctypes.byref(out)), "mla_device_cu_count")
+    return int(out.value)
+
+
+def store_rows(cache, indices, x, stream=None) -> None:
+    """``cache[indices[i]] = x[i]`` over the leading dim; rows are the remaining dims."""
+    import torch
+
+    assert cache.is_cuda and x.is_cuda and indices.is_cuda, "store_rows needs device tensors"
+    assert cache.dtype == x.dtype, "cache and x dtypes differ"
+    n = x.shape[0]
+    row_bytes = x[0].numel() * x.element_size() if n else cache[0].numel() * cache.element_size()
+    assert cache[0].numel() * cache.element_size() == row_bytes, "row widths differ"
+    assert indices.dim() == 1 and indices.shape[0] == n and indices.dtype in (torch.int32, torch.int64)
+    x2 = x.reshape(n, -1) if n else x
+    c2 = cache.view(cache.shape[0], -1)
+    assert x2.stride(-1) == 1 and c2.stride(-1) == 1, "rows must be contiguous"
+    check(
+        load_library().mla_store_rows(
+            _ptr(c2), c2.shape[0], c2.stride(0) * c2.element_size(), _ptr(x2),
+            (x2.stride(0) if n else row_bytes // x.element_size()) * x.element_size(), _ptr(indices),
+            32 if indices.dtype == torch.int32 else 64, n, row_bytes, _stream(stream),
+        ),
+        "mla_store_rows",
+    )
+
+
+def page_table_from_tokens(token_table, table_idx, max_seqlen_k: int, page_size: int, out=None, stream=None):
+    """Device page table ``[B, ceil(max_seqlen_k / ps)]`` from the token-level table."""
+    import torch
+
+    assert token_table.dtype == torch.int32 and table_idx.dtype == torch.int32
+    assert token_table.stride(-1) == 1
+    B = table_idx.shape[0]
+    cols = -(-max_seqlen_k // page_size)
+    if out is None:
+        out = torch.empty((B, cols), dtype=torch.int32, device=token_table.device)
+    check(
+        load_library().mla_page_table_from_tokens(
+            _ptr(token_table), token_table.shape[0], token_table.shape[1], token_table.stride(0),
+            _ptr(table_idx), B, max_seqlen_k, page_size, _ptr(out), out.stride(0), _stream(stream),
+        ),
+        "mla_page_table_from_tokens",
+    )
+    return out
+
+
+def decode_plan(
+    seq_lens, page_size: int, num_ctas: int, max_piece_pages: int = MAX_PIECE_PAGES
+) -> Tuple[np.ndarray, int]:
+    """Host split-KV plan: int32 ``[num_ctas*4 + B*3]`` (CTA ranges, then request info), slots."""
+    lens = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.int32))
+    B = int(lens.shape[0])
+    plan = np.zeros(num_ctas * PLAN_CTA_INTS + B * PLAN_REQ_INTS, dtype=np.int32)
+    slots = ctypes.c_int32(0)
+    cta = plan[: num_ctas * PLAN_CTA_INTS]
+    req = plan[num_ctas * PLAN_CTA_INTS :]
+    p32 = lambda a: a.ctypes.data_as(_c_i32p)  # noqa: E731
+    check(
+        load_library().mla_decode_plan(
+            p32(lens), B, page_size, num_ctas, max_piece_pages, p32(cta),
+            p32(req) if B else None, ctypes.byref(slots),
+        ),
+        "mla_decode_plan",
+    )
+    return plan, int(slots.value)
+
+
+def mla_decode(
+    q, kv_pool, page_table, seq_lens, plan, num_ctas: int, ws_o, ws_lse, scale: float, out, lse=None,
+    stream=None,
+) -> None:
+    """Absorbed-MLA decode: ``q [B, H, 576]``, ``kv_pool [pages, ps, 576]`` -> ``out [B, H, 512]``."""
+    import torch
+
+    B, H, D = q.shape
+    assert D == 576 and kv_pool.shape[-1] == 576 and q.dtype == torch.bfloat16 and kv_pool.dtype == torch.bfloat16
+    assert q.stride(-1) == 1 and kv_pool.stride(-1) == 1
+    assert kv_pool.stride(0) == kv_pool.shape[1] * kv_pool.stride(1), "pool pages must be row-contiguous"
+    assert page_table.dtype == torch.int32 and seq_lens.dtype == torch.int32 and plan.dtype == torch.int32
+    assert out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.stride(-1) == 1
+    assert plan.numel() >= num_ctas * PLAN_CTA_INTS + B * PLAN_REQ_INTS
+    ws_slots = 0 if ws_o is None else ws_o.shape[0]
+    if ws_o is not None:
+        assert ws_o.shape[1:] == (H, 512) and ws_lse.shape[:2] == (ws_slots, H)
+        assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32
+    if lse is not None:
+        assert lse.dtype == torch.float32 and lse.shape == (B, H) and lse.stride(-1) == 1
+    check(
+        load_library().mla_decode_bf16(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(kv_pool), kv_pool.stride(1),
+            kv_pool.shape[0], kv_pool.shape[1], _ptr(page_table), page_table.stride(0), _ptr(seq_lens), B, H,
+            float(scale), _ptr(plan), num_ctas, _ptr(ws_o), _ptr(ws_lse), ws_slots, _ptr(out), out.stride(0),
+            out.stride(1), _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
+        ),
+        "mla_decode_bf16",
+    )
+
+
+def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None) -> None:
+    """fp32 LSE merge of partials ``ws_o [S, H, 512]`` / ``ws_lse [S, H]`` per ``req_info``."""
+    B, H = out.shape[0], out.shape[1]
+    check(
+        load_library().mla_decode_merge_f32(
+            _ptr(ws_o), _ptr(ws_lse), ws_o.shape[0], _ptr(req_info), B, H, _ptr(out), out.stride(0), out.stride(1),
+            _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
+        ),
+        "mla_decode_merge_f32",
+    )

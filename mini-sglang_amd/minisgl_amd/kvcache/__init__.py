@@ -1,0 +1,35 @@
+"""KV pools. ``create_kvcache_pool`` mirrors python/minisgl/kvcache/__init__.py:27-44
+with the MLA variant that the reference leaves as a TODO."""
+
+from __future__ import annotations
+
+import torch
+
+from ..config import MLAConfig
+from .base import BaseKVCachePool
+from .mla_pool import MLAKVCache
+
+
+def create_kvcache_pool(
+    model_config: MLAConfig,
+    num_pages: int,
+    page_size: int,
+    dtype: torch.dtype,
+    device: torch.device,
+    with_prefill_pages: bool = False,
+) -> BaseKVCachePool:
+    return MLAKVCache(
+        num_layers=model_config.num_layers,
+        num_pages=num_pages,
+        page_size=page_size,
+        dtype=dtype,
+        device=device,
+        kv_lora_rank=model_config.kv_lora_rank,
+        qk_rope_head_dim=model_config.qk_rope_head_dim,
+        prefill_heads=model_config.num_heads if with_prefill_pages else 0,
+        qk_head_dim=model_config.qk_head_dim,
+        v_head_dim=model_config.v_head_dim,
+    )
+
+
+__all__ = ["BaseKVCachePool", "MLAKVCache", "create_kvcache_pool"]

@@ -1,0 +1,123 @@
+"""The MLA backend through mini-sglang's interface on the GPU: metadata from a
+batch, store + decode per layer, and HIP-graph capture/replay with static
+buffers (python/minisgl/engine/graph.py:105-158 drives the same hooks)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from minisgl_amd.attention import create_attention_backend
+from minisgl_amd.config import MLAConfig
+from minisgl_amd.core import Batch, Context, Req, reset_global_ctx, set_global_ctx
+from minisgl_amd.kvcache import create_kvcache_pool
+from oracle import ref_mla as R
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+O_TOL = dict(atol=2e-2, rtol=2e-2)
+LSE_TOL = dict(atol=1e-3, rtol=0.0)
+
+
+def _setup(page_size=64, max_req=8, max_seq_len=4096, cached=(100, 1, 640, 3000, 64, 7), seed=0):
+    reset_global_ctx()
+    ctx = Context(page_size=page_size)
+    set_global_ctx(ctx)
+    gen = torch.Generator().manual_seed(seed)
+    cfg = MLAConfig(num_heads=64, num_layers=2)
+    need = [-(-(L + 4) // page_size) for L in cached]  # room for a few decode steps
+    num_pages = sum(need) + 8
+    pool = create_kvcache_pool(cfg, num_pages + 1, page_size, torch.bfloat16, DEV)  # +1 dummy page
+    ctx.kv_cache = pool
+    width = -(-max_seq_len // 32) * 32
+    tt = torch.zeros((max_req + 1, width), dtype=torch.int32)
+    starts = torch.randperm(num_pages, generator=gen)[: sum(need)] * page_size
+    off = 0
+    for r, n in enumerate(need):  # token table as the reference's CacheManager writes it
+        toks = (starts[off : off + n].unsqueeze(1) + torch.arange(page_size)).flatten()
+        tt[r, : n * page_size] = toks.to(torch.int32)
+        off += n
+    tt[max_req].fill_(num_pages * page_size)  # dummy request -> dummy page
+    ctx.page_table = tt.to(DEV)
+    for layer in range(2):
+        pool.latent_cache(layer).copy_(
+            torch.randn(pool.latent_cache(layer).shape, generator=gen).to(torch.bfloat16).to(DEV)
+        )
+    reqs = [Req(table_idx=i, cached_len=L, device_len=L + 1) for i, L in enumerate(cached)]
+    backend = create_attention_backend("mla", cfg)
+    ctx.attn_backend = backend
+    return ctx, cfg, pool, backend, reqs, tt, max_req
+
+
+def _expected(pool, tt, reqs, q, layer, page_size):
+    lens = [r.device_len for r in reqs]
+    idx = torch.tensor([r.table_idx for r in reqs], dtype=torch.int32)
+    pt = R.page_table_from_tokens(tt, idx, max(lens), page_size)
+    return R.mla_decode(q.cpu(), pool.latent_cache(layer).cpu(), pt, lens)
+
+
+def test_backend_decode_eager():
+    ctx, cfg, pool, backend, reqs, tt, _ = _setup()
+    gen = torch.Generator().manual_seed(1)
+    batch = Batch(reqs=reqs, phase="decode")
+    batch.padded_reqs = reqs
+    batch.out_loc = torch.tensor([int(tt[r.table_idx, r.device_len - 1]) for r in reqs], dtype=torch.int32, device=DEV)
+    backend.prepare_metadata(batch)
+    q = torch.randn((len(reqs), 64, 576), generator=gen).to(torch.bfloat16).to(DEV)
+    k_new = torch.randn((len(reqs), 576), generator=gen).to(torch.bfloat16).to(DEV)
+    with ctx.forward_batch(batch):
+        o = backend.forward(q, k_new, k_new[:, :512], 1, batch)
+    torch.cuda.synchronize()
+    # the new latent rows were stored bit-exactly at out_loc
+    flat = pool.latent_cache(1).view(-1, 576)
+    assert torch.equal(flat[batch.out_loc.long()].view(torch.int16), k_new.view(torch.int16))
+    o_ref, lse_ref = _expected(pool, tt, reqs, q, 1, ctx.page_size)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
+    md = batch.attn_metadata
+    assert torch.equal(md.get_last_indices(len(reqs)).cpu(), torch.arange(len(reqs), dtype=torch.int32))
+
+
+def test_backend_decode_graph_replay():
+    ctx, cfg, pool, backend, reqs, tt, max_req = _setup(seed=2)
+    bs = 8
+    dummy = Req(table_idx=max_req, cached_len=0, device_len=1)
+    backend.init_capture_graph(max_seq_len=4096, bs_list=[bs])
+    q_static = torch.zeros((bs, 64, 576), dtype=torch.bfloat16, device=DEV)
+    k_static = torch.zeros((bs, 576), dtype=torch.bfloat16, device=DEV)
+    loc_static = torch.full((bs,), int(tt[max_req, 0]), dtype=torch.int32, device=DEV)
+    cap = Batch(reqs=[dummy] * bs, phase="decode")
+    cap.padded_reqs = cap.reqs
+    cap.out_loc = loc_static
+    backend.prepare_for_capture(cap)
+    stream = torch.cuda.Stream()
+    with ctx.forward_batch(cap), torch.cuda.stream(stream):
+        backend.forward(q_static, k_static, None, 0, cap)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            o_static = backend.forward(q_static, k_static, None, 0, cap)
+    torch.cuda.synchronize()
+
+    gen = torch.Generator().manual_seed(3)
+    for step in range(3):
+        live = Batch(reqs=reqs, phase="decode")
+        live.padded_reqs = reqs + [dummy] * (bs - len(reqs))
+        live.out_loc = torch.tensor(
+            [int(tt[r.table_idx, r.device_len - 1]) for r in live.padded_reqs], dtype=torch.int32, device=DEV
+        )
+        backend.prepare_metadata(live)
+        backend.prepare_for_replay(live)
+        q = torch.randn((bs, 64, 576), generator=gen).to(torch.bfloat16).to(DEV)
+        k_new = torch.randn((bs, 576), generator=gen).to(torch.bfloat16).to(DEV)
+        q_static.copy_(q)
+        k_static.copy_(k_new)
+        loc_static.copy_(live.out_loc)
+        g.replay()
+        torch.cuda.synchronize()
+        n = len(reqs)
+        o_ref, lse_ref = _expected(pool, tt, reqs, q[:n], 0, ctx.page_size)
+        torch.testing.assert_close(o_static[:n].float().cpu(), o_ref, **O_TOL)
+        # eager work between replays, then the requests advance by one token
+        _ = (q.float() * 2).sum().item()
+        for r in reqs:
+            r.complete_one()

@@ -1,0 +1,157 @@
+"""GPU parity of the absorbed-MLA decode path (HIP kernels via the C ABI)
+against the CPU oracle and the committed golden fixture.
+
+Tolerances: bf16 output atol = rtol = 2e-2; fp32 natural-log LSE atol 1e-3;
+store, page-table gather bit-exact.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from minisgl_amd.benchmark.inputs import make_decode_case
+from minisgl_amd.kernel import lib
+from oracle import ref_mla as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+HERE = os.path.dirname(os.path.abspath(__file__))
+O_TOL = dict(atol=2e-2, rtol=2e-2)
+LSE_TOL = dict(atol=1e-3, rtol=0.0)
+
+
+def run_decode(q, kv, pt, seq_lens, lens, ps, num_ctas, scale=R.DEFAULT_SCALE):
+    B, H, _ = q.shape
+    plan_np, slots = lib.decode_plan(lens, ps, num_ctas)
+    plan = torch.from_numpy(plan_np).to(DEV)
+    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=DEV)
+    ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=DEV)
+    out = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((B, H), float("nan"), dtype=torch.float32, device=DEV)
+    lib.mla_decode(q, kv, pt, seq_lens, plan, num_ctas, ws_o, ws_lse, scale, out, lse)
+    torch.cuda.synchronize()
+    return out.float().cpu(), lse.cpu(), slots
+
+
+def check_case(case, num_ctas):
+    o_ref, lse_ref = R.mla_decode(case.q, case.kv_pool, case.page_table, case.lens)
+    out, lse, _ = run_decode(
+        case.q.to(DEV), case.kv_pool.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV), case.lens,
+        case.page_size, num_ctas,
+    )
+    nonempty = torch.tensor([L > 0 for L in case.lens])
+    torch.testing.assert_close(out[nonempty], o_ref[nonempty], **O_TOL)
+    torch.testing.assert_close(lse[nonempty], lse_ref[nonempty], **LSE_TOL)
+    if (~nonempty).any():
+        assert torch.all(out[~nonempty] == 0) and torch.all(torch.isneginf(lse[~nonempty]))
+
+
+@pytest.mark.parametrize("num_ctas", [256, 7])
+def test_decode_cpu_reference_shape(num_ctas):
+    """B=4, 16 heads, page_size 1, lengths U[64, 512] (the CPU-reference workload)."""
+    case = make_decode_case(4, 16, 1, len_range=(64, 512))
+    check_case(case, num_ctas)
+
+
+@pytest.mark.parametrize("num_ctas", [256, 5, 1])
+def test_decode_ragged_edges_ps64(num_ctas):
+    case = make_decode_case(8, 64, 64, lens=[1, 31, 32, 33, 63, 64, 65, 1000])
+    check_case(case, num_ctas)
+
+
+@pytest.mark.parametrize("heads,ps", [(32, 16), (48, 32), (16, 128), (64, 2)])
+def test_decode_heads_and_page_sizes(heads, ps):
+    case = make_decode_case(5, heads, ps, len_range=(1, 700), seed=heads + ps)
+    check_case(case, 64)
+
+
+def test_decode_long_split_merge():
+    """Long requests split over many CTAs exercise the LSE merge kernel."""
+    case = make_decode_case(3, 64, 64, lens=[20000, 4097, 130], seed=3)
+    check_case(case, 96)
+
+
+def test_decode_empty_request():
+    case = make_decode_case(3, 16, 16, lens=[5, 0, 100], seed=4)
+    check_case(case, 16)
+
+
+def test_decode_golden_fixture():
+    f = np.load(os.path.join(HERE, "golden", "decode_small.npz"))
+    bf = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)  # noqa: E731
+    q, kv = bf(f["q_bits"]).to(DEV), bf(f["kv_bits"]).to(DEV)
+    lens = f["seq_lens"].tolist()
+    for ctas in (1, 3, 256):
+        out, lse, _ = run_decode(q, kv, torch.from_numpy(f["page_table"]).to(DEV),
+                                 torch.from_numpy(f["seq_lens"]).to(DEV), lens, int(f["page_size"]), ctas,
+                                 float(f["scale"]))
+        torch.testing.assert_close(out, torch.from_numpy(f["o"]), **O_TOL)
+        torch.testing.assert_close(lse.double(), torch.from_numpy(f["lse"]), **LSE_TOL)
+
+
+def test_decode_large_logits_rescale():
+    """Scores that grow along the sequence force the softmax rescale path."""
+    case = make_decode_case(2, 16, 64, lens=[900, 2000], seed=9)
+    ramp = torch.linspace(0, 30, case.kv_pool.shape[0] * 64).view(-1, 64, 1)
+    kv = case.kv_pool.float()
+    kv[..., 512:513] = ramp  # rope column grows with the flat row index
+    case.kv_pool = kv.to(torch.bfloat16)
+    case.q[..., 512] = 20.0
+    check_case(case, 8)
+
+
+def test_merge_kernel_standalone():
+    gen = torch.Generator().manual_seed(5)
+    H, S = 16, 11
+    o_parts = torch.randn((S, H, 512), generator=gen)
+    lse_parts = torch.randn((S, H), generator=gen) * 3
+    lse_parts[4] = float("-inf")  # an empty piece
+    req_info = torch.tensor([[0, 3, 0], [0, 1, 3], [0, 0, 0], [0, 7, 4]], dtype=torch.int32)
+    out = torch.empty((4, H, 512), dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty((4, H), dtype=torch.float32, device=DEV)
+    lib.mla_decode_merge(o_parts.to(DEV), lse_parts.to(DEV), req_info.flatten().to(DEV), out, lse)
+    torch.cuda.synchronize()
+    for b, (_, n, base) in enumerate(req_info.tolist()):
+        o_ref, l_ref = R.mla_merge(o_parts[base : base + n], lse_parts[base : base + n])
+        torch.testing.assert_close(out[b].float().cpu(), o_ref, **O_TOL)
+        torch.testing.assert_close(lse[b].cpu(), l_ref, **LSE_TOL)
+
+
+@pytest.mark.parametrize("row_elems,index_dtype", [(576, torch.int32), (576, torch.int64), (64 * 192, torch.int32)])
+def test_store_rows_bit_exact(row_elems, index_dtype):
+    gen = torch.Generator().manual_seed(row_elems)
+    rows = 4096
+    cache = torch.randn((rows, row_elems), generator=gen).to(torch.bfloat16).to(DEV)
+    before = cache.clone()
+    for n in (1, 7, 64, 1000):
+        idx = torch.randperm(rows, generator=gen)[:n].to(index_dtype)
+        x = torch.randn((n, row_elems), generator=gen).to(torch.bfloat16).to(DEV)
+        lib.store_rows(cache, idx.to(DEV), x)
+        torch.cuda.synchronize()
+        ref = before.cpu().clone()
+        R.store_rows(ref, idx, x.cpu())
+        assert torch.equal(cache.cpu().view(torch.int16), ref.view(torch.int16)), n
+        before = cache.clone()
+
+
+def test_page_table_kernel_bit_exact():
+    f = np.load(os.path.join(HERE, "golden", "page_table_small.npz"))
+    tt = torch.from_numpy(f["token_table"]).to(DEV)
+    got = lib.page_table_from_tokens(tt, torch.from_numpy(f["table_idx"]).to(DEV), int(f["max_seqlen_k"]),
+                                     int(f["page_size"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), f["page_table"])
+    # random tables at page sizes 1 and 64
+    gen = torch.Generator().manual_seed(1)
+    for ps in (1, 64):
+        tt = torch.randint(0, 1 << 20, (9, 4096), generator=gen, dtype=torch.int32)
+        idx = torch.randint(0, 9, (13,), generator=gen, dtype=torch.int32)
+        ref = R.page_table_from_tokens(tt, idx, 4000, ps)
+        got = lib.page_table_from_tokens(tt.to(DEV), idx.to(DEV), 4000, ps)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), ref)
