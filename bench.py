@@ -1,0 +1,202 @@
+"""Benchmark of the MLA attention hot path on one MI355X.
+
+Default workload (the headline one): Kimi-K2-shape absorbed-MLA paged decode,
+batch 64, 64 heads, 576-dim q / latent KV, page_size 64, random
+non-contiguous page table, seq_lens ~ U[1024, 8192], bf16 N(0,1) inputs.
+A "step" is one layer's decode attention over the batch: the split-KV
+kernel plus the LSE merge kernel, inputs resident in HBM. Two input sets
+(680 MB of KV together, more than the 256 MB Infinity Cache) alternate so
+every step streams its KV from HBM.
+
+Prints one JSON line. ``value`` is the whole-step algorithmic HBM bandwidth
+(TB/s); µs/layer and tokens/s are extra fields. ``roofline`` times the
+dominant kernel (the split kernel) with HIP events on its launch stream.
+``cpu_baseline`` times the CPU oracle on a bounded sample of the same batch.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "mini-sglang_amd")]
+
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mla_decode_kimi_k2_b64_traffic.json")
+
+
+def _decode_workload(device, seed):
+    from minisgl_amd.benchmark.inputs import make_decode_case
+
+    return make_decode_case(64, 64, 64, len_range=(1024, 8192), device=device, seed=seed)
+
+
+def _cpu_baseline(case_gpu, budget_s: float = 12.0):
+    """Oracle (fp32 torch on the host cores) on the first n requests of the batch."""
+    import torch
+
+    from oracle import ref_mla as R
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    q = case_gpu.q.cpu()
+    kv = case_gpu.kv_pool.cpu()
+    pt = case_gpu.page_table.cpu()
+    lens = case_gpu.lens
+    R.mla_decode(q[:1], kv, pt[:1], lens[:1])  # warm-up
+    t0 = time.perf_counter()
+    R.mla_decode(q[:1], kv, pt[:1], lens[:1])
+    per_req = max(time.perf_counter() - t0, 1e-4)
+    n = int(max(1, min(len(lens), budget_s / per_req)))
+    reps, elapsed = 0, 0.0
+    t0 = time.perf_counter()
+    while True:
+        R.mla_decode(q[:n], kv, pt[:n], lens[:n])
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed > budget_s or reps >= 3:
+            break
+    sec = elapsed / reps
+    H = q.shape[1]
+    pages = sum(-(-L // 64) for L in lens[:n])
+    sample_bytes = sum(lens[:n]) * 1152 + n * H * (576 + 512) * 2 + n * H * 4 + pages * 4 + 4 * n
+    return {
+        "value": sample_bytes / sec / 1e12,
+        "unit": "TB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"CPU oracle (oracle/ref_mla.py, fp32 torch) on requests 0..{n - 1} of the same batch "
+        f"({sum(lens[:n])} KV tokens), {reps} run(s), {sec * 1e3:.1f} ms each",
+        "us_per_layer_sample": sec * 1e6,
+    }
+
+
+def bench_decode(args):
+    import torch
+
+    from minisgl_amd.kernel import lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sets = [_decode_workload(dev, 0)]
+    from minisgl_amd.benchmark.inputs import make_decode_case
+
+    # second input set: same lengths (so the same plan and work), different pages and values
+    sets.append(make_decode_case(64, 64, 64, lens=sets[0].lens, device=dev, seed=100))
+    case = sets[0]
+    B, H, _ = case.q.shape
+    ctas = lib.device_cu_count(0)
+    plan_np, slots = lib.decode_plan(case.lens, case.page_size, ctas)
+    plan = torch.from_numpy(plan_np).to(dev)
+    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=dev)
+    ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=dev)
+    out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev)
+    req_info = plan[ctas * lib.PLAN_CTA_INTS :]
+    scale = (128 + 64) ** -0.5
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        s = sets[i % 2]
+        if ev is not None:
+            ev[0].record(stream)
+        lib.mla_decode(s.q, s.kv_pool, s.page_table, s.seq_lens, plan, ctas, ws_o, ws_lse, scale, out, lse,
+                       stream=stream, split_only=True)
+        if ev is not None:
+            ev[1].record(stream)
+        lib.mla_decode_merge(ws_o, ws_lse, req_info, out, lse, stream=stream, single_piece_final=True)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    split_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    merge_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    step_ms = wall * 1e3 / args.steps
+    dev_step_ms = events[0][0].elapsed_time(events[-1][2]) / args.steps
+
+    alg_bytes = case.algorithmic_bytes()
+    value_tbps = alg_bytes / (step_ms * 1e-3) / 1e12
+    achieved = alg_bytes / (split_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    result = {
+        "metric": "MLA decode achieved HBM TB/s + us/layer, Kimi-K2 shape, 1 MI355X",
+        "value": round(value_tbps, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 q and latent KV, random page table)",
+        "config": {
+            "workload": "Kimi-K2-shape absorbed-MLA paged decode, one layer (split-KV + LSE merge)",
+            "batch": B,
+            "heads": H,
+            "kv_dim": 576,
+            "v_dim": 512,
+            "page_size": case.page_size,
+            "seq_len_range": [1024, 8192],
+            "kv_tokens": sum(case.lens),
+            "input_sets": len(sets),
+            "num_ctas": ctas,
+            "partial_slots": slots,
+        },
+        "us_per_layer": round(step_ms * 1e3, 2),
+        "us_per_layer_device": round(dev_step_ms * 1e3, 2),
+        "tokens_per_s": round(B / (step_ms * 1e-3), 1),
+        "split_kernel_us": round(split_ms * 1e3, 2),
+        "merge_kernel_us": round(merge_ms * 1e3, 2),
+        "algorithmic_bytes_per_step": alg_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "mla_decode_kernel<4,true> (split step)",
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = _cpu_baseline(case)
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part "
+              "of this build", file=sys.stderr)
+        sys.exit(2)
+    res = bench_decode(args)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

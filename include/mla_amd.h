@@ -121,16 +121,33 @@ int mla_decode_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h, const
                     void *stream);
 
 /*
- * fp32 log-sum-exp merge of split-KV partials (standalone form of the merge
- * step of mla_decode_bf16). For request b with n = req_info[3b+1] pieces in
- * slots s = req_info[3b+2] .. +n-1:
+ * The split step of mla_decode_bf16 alone (same arguments): requests covered
+ * by one piece get their final bf16 output and LSE, split requests leave
+ * normalised fp32 partials in ws_o / ws_lse for mla_decode_merge_f32 with
+ * single_piece_final = 1. No counterpart in the reference (its decode is one
+ * opaque library call); it is the unit a sequence-sharded decode distributes.
+ */
+int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                          const void *kv_pool, int64_t kv_row_stride, int32_t num_pages,
+                          int32_t page_size, const int32_t *page_table, int64_t pt_stride,
+                          const int32_t *seq_lens, int32_t batch, int32_t heads, float scale,
+                          const int32_t *plan, int32_t num_ctas, float *ws_o, float *ws_lse,
+                          int32_t ws_slots, void *out, int64_t out_stride_b,
+                          int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
+
+/*
+ * fp32 log-sum-exp merge of split-KV partials (the merge step of
+ * mla_decode_bf16). For request b with n = req_info[3b+1] pieces in slots
+ * s = req_info[3b+2] .. +n-1:
  *   lse = ln sum_i exp(ws_lse[s_i]);  out = sum_i exp(ws_lse[s_i] - lse) * ws_o[s_i]
- * n == 0 writes out = 0, lse = -inf.
+ * n == 0 writes out = 0, lse = -inf. With single_piece_final != 0 requests
+ * with n == 1 are skipped (the split step already wrote them); otherwise
+ * their one slot is converted like any other.
  */
 int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slots,
-                         const int32_t *req_info, int32_t batch, int32_t heads, void *out,
-                         int64_t out_stride_b, int64_t out_stride_h, float *lse,
-                         int64_t lse_stride_b, void *stream);
+                         const int32_t *req_info, int32_t batch, int32_t heads,
+                         int32_t single_piece_final, void *out, int64_t out_stride_b,
+                         int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
 
 #ifdef __cplusplus
 }

@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 1; }
+int mla_abi_version(void) { return 2; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -110,14 +110,18 @@ int mla_page_table_from_tokens(const int32_t* token_table, int32_t token_table_r
 }
 
 // Greedy contiguous partition of the requests' blocks with at most `cap`
-// cost units (blocks + kPieceOverheadBlocks per piece) per CTA and at most
-// max_blk blocks per piece. Returns the number of CTAs used, or INT32_MAX if a
-// CTA would overflow `limit` CTAs. Writes the plan when `write` is set.
+// cost units (blocks + kPieceOverheadBlocks per piece) per CTA, at most
+// max_blk blocks per piece, and per CTA at most mla::kMaxCtaBlocks blocks and
+// mla::kMaxCtaRequests requests (the streaming kernel stages per-tile page ids
+// and per-request bounds of its range in LDS). Returns the number of CTAs
+// used, or INT32_MAX if the partition needs more than `limit` CTAs. Writes the
+// plan when `write` is set.
 static int plan_greedy(const int32_t* seq_lens, int batch, int64_t cap, int64_t max_blk, int limit, bool write,
                        int32_t* cta_ranges, int32_t* req_info, int32_t* num_slots) {
   const int B = mla::kPlanBlock;
   int w = 0;
-  int64_t used = 0;
+  int64_t used = 0, blocks = 0;
+  int reqs = 0;
   int32_t slots = 0;
   if (write) {
     cta_ranges[0] = 0;
@@ -132,18 +136,23 @@ static int plan_greedy(const int32_t* seq_lens, int batch, int64_t cap, int64_t 
       cta_ranges[4 * (w + 1) + 1] = (int32_t)blk;
     }
     ++w;
-    used = 0;
+    used = blocks = 0;
+    reqs = 0;
     return true;
   };
   for (int b = 0; b < batch; ++b) {
     const int64_t nb = ((int64_t)seq_lens[b] + B - 1) / B;
     int first = w, pieces = 0;
     int64_t blk = 0;
+    if (reqs >= mla::kMaxCtaRequests && !next_cta(b, 0)) return INT32_MAX;
+    ++reqs;  // every request of the range (even an empty one) has an LDS entry
     while (blk < nb) {
-      const int64_t room = cap - used - kPieceOverheadBlocks;
+      int64_t room = cap - used - kPieceOverheadBlocks;
+      if (room > mla::kMaxCtaBlocks - blocks) room = mla::kMaxCtaBlocks - blocks;
       if (room <= 0) {
         if (used == 0) return INT32_MAX;  // cap too small for any block
         if (!next_cta(b, blk)) return INT32_MAX;
+        ++reqs;
         continue;
       }
       int64_t take = nb - blk;
@@ -153,7 +162,11 @@ static int plan_greedy(const int32_t* seq_lens, int batch, int64_t cap, int64_t 
       ++pieces;
       blk += take;
       used += take + kPieceOverheadBlocks;
-      if (blk < nb && !next_cta(b, blk)) return INT32_MAX;
+      blocks += take;
+      if (blk < nb) {
+        if (!next_cta(b, blk)) return INT32_MAX;
+        ++reqs;
+      }
     }
     if (write) {
       req_info[3 * b + 0] = first;
@@ -228,15 +241,12 @@ static int check_out(const void* out, int64_t sb, int64_t sh, const float* lse, 
   return MLA_OK;
 }
 
-int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
-                    int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
-                    int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
-                    void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
-                    void* stream) {
-  const char* who = "mla_decode_bf16";
-  if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
-  if (batch == 0) return ok();
+static int decode_params(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         const void* kv_pool, int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
+                         const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens, int32_t batch,
+                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, float* ws_o,
+                         float* ws_lse, int32_t ws_slots, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                         float* lse, int64_t lse_stride_b, mla::DecodeParams* p) {
   if (heads != 16 && heads != 32 && heads != 48 && heads != 64)
     return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be 16, 32, 48 or 64, got %d", who, heads);
   if (q == nullptr || kv_pool == nullptr || page_table == nullptr || seq_lens == nullptr || plan == nullptr)
@@ -244,9 +254,9 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
   if (!aligned(q, 16) || q_stride_h % 8 != 0 || q_stride_b % 8 != 0 || q_stride_h < MLA_KV_DIM ||
       q_stride_b < (int64_t)heads * q_stride_h)
     return fail(MLA_ERR_INVALID_ARG, "%s: q must be 16-byte aligned, row-contiguous, strides multiples of 8", who);
-  if (!aligned(kv_pool, 16) || kv_row_stride % 8 != 0 || kv_row_stride < MLA_KV_DIM)
-    return fail(MLA_ERR_INVALID_ARG, "%s: kv_pool must be 16-byte aligned with row stride >= 576, multiple of 8",
-                who);
+  if (!aligned(kv_pool, 16) || kv_row_stride % 8 != 0 || kv_row_stride < MLA_KV_DIM || kv_row_stride > (1 << 20))
+    return fail(MLA_ERR_INVALID_ARG,
+                "%s: kv_pool must be 16-byte aligned with row stride in [576, 2^20], multiple of 8", who);
   if (num_pages < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages must be >= 1", who);
   if (!is_pow2(page_size)) return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d is not a power of two", who, page_size);
   if (pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: pt_stride must be >= 1", who);
@@ -256,60 +266,36 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
     return fail(MLA_ERR_INVALID_ARG, "%s: workspace pointers are null", who);
   if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
   if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
-
-  mla::DecodeParams p;
-  p.q = static_cast<const __bf16*>(q);
-  p.q_stride_b = q_stride_b;
-  p.q_stride_h = q_stride_h;
-  p.kv = static_cast<const __bf16*>(kv_pool);
-  p.kv_row_stride = kv_row_stride;
-  p.num_pages = num_pages;
-  p.log2_ps = ilog2(page_size);
-  p.page_table = page_table;
-  p.pt_stride = pt_stride;
-  p.seq_lens = seq_lens;
-  p.batch = batch;
-  p.heads = heads;
-  p.scale_log2 = scale * 1.4426950408889634f;
-  p.plan = plan;
-  p.num_ctas = num_ctas;
-  p.ws_o = ws_o;
-  p.ws_lse = ws_lse;
-  p.ws_slots = ws_slots;
-  p.out = static_cast<__bf16*>(out);
-  p.out_stride_b = out_stride_b;
-  p.out_stride_h = out_stride_h;
-  p.lse = lse;
-  p.lse_stride_b = lse_stride_b;
-  hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
-
-  mla::MergeParams m;
-  m.ws_o = ws_o;
-  m.ws_lse = ws_lse;
-  m.ws_slots = ws_slots;
-  m.req_info = plan + 4 * (int64_t)num_ctas;
-  m.batch = batch;
-  m.heads = heads;
-  m.skip_single = 1;
-  m.out = p.out;
-  m.out_stride_b = out_stride_b;
-  m.out_stride_h = out_stride_h;
-  m.lse = lse;
-  m.lse_stride_b = lse_stride_b;
-  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch");
+  p->q = static_cast<const __bf16*>(q);
+  p->q_stride_b = q_stride_b;
+  p->q_stride_h = q_stride_h;
+  p->kv = static_cast<const __bf16*>(kv_pool);
+  p->kv_row_stride = kv_row_stride;
+  p->num_pages = num_pages;
+  p->log2_ps = ilog2(page_size);
+  p->page_table = page_table;
+  p->pt_stride = pt_stride;
+  p->seq_lens = seq_lens;
+  p->batch = batch;
+  p->heads = heads;
+  p->scale_log2 = scale * 1.4426950408889634f;
+  p->plan = plan;
+  p->num_ctas = num_ctas;
+  p->ws_o = ws_o;
+  p->ws_lse = ws_lse;
+  p->ws_slots = ws_slots;
+  p->out = static_cast<__bf16*>(out);
+  p->out_stride_b = out_stride_b;
+  p->out_stride_h = out_stride_h;
+  p->lse = lse;
+  p->lse_stride_b = lse_stride_b;
+  return MLA_OK;
 }
 
-int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
-                         int32_t batch, int32_t heads, void* out, int64_t out_stride_b, int64_t out_stride_h,
-                         float* lse, int64_t lse_stride_b, void* stream) {
-  const char* who = "mla_decode_merge_f32";
-  if (batch < 0 || heads < 1 || ws_slots < 0) return fail(MLA_ERR_INVALID_ARG, "%s: invalid sizes", who);
-  if (batch == 0) return ok();
-  if (req_info == nullptr || (ws_slots > 0 && (ws_o == nullptr || ws_lse == nullptr)))
-    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
-  if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
-  if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
+static mla::MergeParams merge_params(const float* ws_o, const float* ws_lse, int32_t ws_slots,
+                                     const int32_t* req_info, int32_t batch, int32_t heads, int32_t skip_single,
+                                     void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
+                                     int64_t lse_stride_b) {
   mla::MergeParams m;
   m.ws_o = ws_o;
   m.ws_lse = ws_lse;
@@ -317,12 +303,65 @@ int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slot
   m.req_info = req_info;
   m.batch = batch;
   m.heads = heads;
-  m.skip_single = 0;
+  m.skip_single = skip_single;
   m.out = static_cast<__bf16*>(out);
   m.out_stride_b = out_stride_b;
   m.out_stride_h = out_stride_h;
   m.lse = lse;
   m.lse_stride_b = lse_stride_b;
+  return m;
+}
+
+int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
+                          int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
+                          int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
+                          const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                          void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
+                          int64_t lse_stride_b, void* stream) {
+  const char* who = "mla_decode_split_bf16";
+  if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
+  if (batch == 0) return ok();
+  mla::DecodeParams p;
+  if (int rc = decode_params(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size, page_table,
+                             pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse, ws_slots, out,
+                             out_stride_b, out_stride_h, lse, lse_stride_b, &p))
+    return rc;
+  return hip_status(mla::launch_decode(p, (hipStream_t)stream), "mla_decode_split_bf16 launch");
+}
+
+int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
+                    int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
+                    int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
+                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                    void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
+                    void* stream) {
+  const char* who = "mla_decode_bf16";
+  if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
+  if (batch == 0) return ok();
+  mla::DecodeParams p;
+  if (int rc = decode_params(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size, page_table,
+                             pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse, ws_slots, out,
+                             out_stride_b, out_stride_h, lse, lse_stride_b, &p))
+    return rc;
+  hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
+  const mla::MergeParams m = merge_params(ws_o, ws_lse, ws_slots, plan + 4 * (int64_t)num_ctas, batch, heads, 1, out,
+                                          out_stride_b, out_stride_h, lse, lse_stride_b);
+  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch");
+}
+
+int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
+                         int32_t batch, int32_t heads, int32_t single_piece_final, void* out, int64_t out_stride_b,
+                         int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
+  const char* who = "mla_decode_merge_f32";
+  if (batch < 0 || heads < 1 || ws_slots < 0) return fail(MLA_ERR_INVALID_ARG, "%s: invalid sizes", who);
+  if (batch == 0) return ok();
+  if (req_info == nullptr || (ws_slots > 0 && (ws_o == nullptr || ws_lse == nullptr)))
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
+  if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
+  const mla::MergeParams m = merge_params(ws_o, ws_lse, ws_slots, req_info, batch, heads, single_piece_final ? 1 : 0,
+                                          out, out_stride_b, out_stride_h, lse, lse_stride_b);
   return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_merge_f32 launch");
 }
 

@@ -27,6 +27,10 @@ constexpr int kTileDma = kTileBytes / 1024;    // 36 wave-wide DMA loads per til
 constexpr int kStages = 4;                     // LDS ring depth (147456 bytes)
 constexpr int kPlanBlock = 64;                 // tokens per plan block
 constexpr int kMaxPieceIds = 1024;             // page ids of one piece staged in LDS
+// Per-CTA limits of a decode plan: the streaming kernel stages one page id per
+// 32-token tile (2 per plan block) and the bounds of every request of its range.
+constexpr int kMaxCtaBlocks = 1024;
+constexpr int kMaxCtaRequests = 128;
 
 struct DecodeParams {
   const __bf16* q;  // [B, H, 576]
@@ -65,6 +69,7 @@ struct MergeParams {
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+hipError_t launch_decode_stream(const DecodeParams& p, hipStream_t stream);  // heads 64, pages >= 32
 hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
 hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
                              const void* indices, int index_bits, int64_t rows, int64_t row_bytes,

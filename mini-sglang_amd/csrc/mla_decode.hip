@@ -24,57 +24,22 @@
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j%4
 // of the 8-byte words addressed by lanes j/4 + 4k, k = 0..3.
 #include "mla_common.h"
+#include "mla_device.h"
 
 namespace mla {
 namespace {
 
-__device__ __forceinline__ int swz(int t7) { return ((t7 & 3) << 1) | ((t7 >> 2) & 1); }
-
-__device__ __forceinline__ float wave_max_g(float v) {
-  // reduce over the 4 lane groups (lanes l, l^16, l^32, l^48)
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
-__device__ __forceinline__ float wave_sum_g(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
-
-// Wait until at most N vector-memory operations of this wave are outstanding.
-// The counter saturates at 63; a smaller count only waits longer, so N is clamped.
-template <int N0>
-__device__ __forceinline__ void wait_vmcnt() {
-  constexpr int N = N0 > 63 ? 63 : N0;
-  static_assert(N >= 0, "vmcnt range");
-  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4]=7 | lgkmcnt[11:8]=15 | vmcnt[5:4] at [15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
-}
-
-// 16-byte global -> LDS DMA; lane i's data lands at LDS byte address
-// lds_base + 16*i. Issued as inline asm so that the compiler's wait-count
-// pass does not serialise later LDS reads of other stages behind it: every
-// read of a staged tile is preceded by wait_vmcnt + a workgroup barrier.
-__device__ __forceinline__ void dma16_saddr(const char* base, uint32_t voff, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
-}
-__device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  // round-to-nearest-even, matching torch's float->bfloat16 conversion
-  __bf16 x = (__bf16)a, y = (__bf16)b;
-  uint16_t ux = __builtin_bit_cast(uint16_t, x), uy = __builtin_bit_cast(uint16_t, y);
-  return (uint32_t)ux | ((uint32_t)uy << 16);
-}
-
-// Softmax rescaling is skipped until a head's running max grows by more than
-// this many log2 units; exp2 of a stale-max score then stays below 2^8.
-constexpr float kRescaleLog2 = 8.0f;
+// Online softmax without rescaling the output accumulators: scores are
+// exponentiated against a fixed per-head reference (the piece's first-tile
+// max), so exp2(x - m_ref) can exceed 1. If any score of a piece exceeds its
+// reference by more than kOverflowLog2 (exp2 would approach the bf16/fp32
+// range), the whole CTA re-runs the piece with the reference set to the
+// piece's exact max, where every exp2 is <= 1. Both runs compute the same
+// normalised result; the second one only happens for extreme logits.
+constexpr float kOverflowLog2 = 64.0f;
 constexpr int kKPrefetch = 8;  // K operands (16-byte LDS reads) in flight
 constexpr int kVPrefetch = 4;  // V operand pairs (transposing LDS reads) in flight
+constexpr int kQkChains = 3;   // independent QK accumulators per 16-token block
 
 template <int NW, bool kPageCoversTile>
 __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodeParams p) {
@@ -84,7 +49,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
   __shared__ int s_ids[kMaxPieceIds];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4;
   const int c = lane & 15;
   const int w = blockIdx.x;
@@ -107,14 +72,16 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
   for (int q4 = 0; q4 < 4; ++q4)
     v_off[q4] = v_row + ((2 * (q4 ^ (c >> 2)) + (((c & 3) >> 1) ^ (g & 1))) << 4) + ((c & 1) << 3);
 
-  // per-lane DMA slot of each of this wave's loads: token t_k, swizzled chunk byte offset
-  int dma_t[kDmaPerWave], dma_c16[kDmaPerWave];
+  // DMA slot s = 64 * load + lane of a tile holds token s / 72, chunk (s % 72) ^ swz(token & 7)
+  auto slot_token = [&](int k) { return (((wave + k * NW) * 64 + lane) * 7282) >> 19; };  // s / 72, s < 2304
+  auto slot_chunk16 = [&](int k, int t) {
+    return (((wave + k * NW) * 64 + lane - t * kRowChunks) ^ swz(t & 7)) << 4;
+  };
+  uint32_t dma_voff[kDmaPerWave];  // byte offset of this lane's chunk from the tile's first row
 #pragma unroll
   for (int k = 0; k < kDmaPerWave; ++k) {
-    const int s = (wave + k * NW) * 64 + lane;
-    const int t = (s * 7282) >> 19;  // s / 72 for s < 2304
-    dma_t[k] = t;
-    dma_c16[k] = ((s - t * kRowChunks) ^ swz(t & 7)) << 4;
+    const int t = slot_token(k);
+    dma_voff[k] = t * row_bytes + slot_chunk16(k, t);
   }
 
   for (int b = rb; b <= re && b < p.batch; ++b) {
@@ -132,6 +99,11 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     bf16x8 qf[18];
 #pragma unroll
     for (int ks = 0; ks < 18; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
+    // Consume Q here so the compiler's vmcnt wait for these loads lands before
+    // the tile loop; at their first use inside the loop it would also wait for
+    // every DMA load in flight (the counter is in order) on every tile.
+#pragma unroll
+    for (int ks = 0; ks < 18; ++ks) asm volatile("" ::"v"(qf[ks]));
 
     // ---- page ids of the piece -> LDS
     const int pg0 = t0 >> p.log2_ps;
@@ -155,134 +127,147 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
         const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (tstart & ps_mask)) * row_bytes;
         if (tlim >= kTile - 1) {
 #pragma unroll
-          for (int k = 0; k < kDmaPerWave; ++k)
-            dma16_saddr(tsrc, dma_t[k] * row_bytes + dma_c16[k], lds_stage + (wave + k * NW) * 1024);
+          for (int k = 0; k < kDmaPerWave; ++k) dma16_saddr(tsrc, dma_voff[k], lds_stage + (wave + k * NW) * 1024);
         } else {
 #pragma unroll
-          for (int k = 0; k < kDmaPerWave; ++k)
-            dma16_saddr(tsrc, min(dma_t[k], tlim) * row_bytes + dma_c16[k], lds_stage + (wave + k * NW) * 1024);
+          for (int k = 0; k < kDmaPerWave; ++k) {
+            const int t = slot_token(k);
+            dma16_saddr(tsrc, min(t, tlim) * row_bytes + slot_chunk16(k, t), lds_stage + (wave + k * NW) * 1024);
+          }
         }
       } else {
 #pragma unroll
         for (int k = 0; k < kDmaPerWave; ++k) {
-          const int tok = tstart + min(dma_t[k], tlim);
+          const int t = slot_token(k);
+          const int tok = tstart + min(t, tlim);
           const int pid = s_ids[(tok >> p.log2_ps) - pg0];
-          const char* src = kv + ((int64_t)pid * (ps_mask + 1) + (tok & ps_mask)) * row_bytes + dma_c16[k];
+          const char* src = kv + ((int64_t)pid * (ps_mask + 1) + (tok & ps_mask)) * row_bytes + slot_chunk16(k, t);
           dma16_vaddr(src, lds_stage + (wave + k * NW) * 1024);
         }
       }
     };
 
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
-      if (s < ntiles) issue(s, s);
-
+    float m_ref = 0.f;     // per-head exponent reference (log2 units)
+    float m_max = -INFINITY;  // per-head max score of the piece
+    float l_run = 0.f;
     f32x4 O[32];
+    for (int attempt = 0; attempt < 2; ++attempt) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
-
-    for (int it = 0; it < ntiles; ++it) {
-      const int ahead = ntiles - 1 - it;  // tiles issued after this one (capped below)
-      if (ahead >= kStages - 2) wait_vmcnt<kDmaPerWave * (kStages - 2)>();
-      else if (ahead == 1) wait_vmcnt<kDmaPerWave>();
-      else wait_vmcnt<0>();
-      __syncthreads();
-      if (it + kStages - 1 < ntiles) issue(it + kStages - 1, (it + kStages - 1) % kStages);
-
-      const MLA_LDS char* T = (const MLA_LDS char*)smem + (it % kStages) * kTileBytes;
-
-      // ---- S^T = K . Q^T : tokens 0-15 (s0) and 16-31 (s1) of the tile.
-      // Read j covers k-step j>>1 of token block j&1.
-      auto kread = [&](int j) {
-        const int ks = j >> 1;
-        const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (j & 1) * 16 * kRowBytes;
-        return *reinterpret_cast<const MLA_LDS bf16x8*>(T + off);
-      };
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      bf16x8 kbuf[kKPrefetch];
+      for (int s = 0; s < kStages - 1; ++s)
+        if (s < ntiles) issue(s, s);
 #pragma unroll
-      for (int j = 0; j < kKPrefetch; ++j) kbuf[j] = kread(j);
-#pragma unroll
-      for (int j = 0; j < 36; ++j) {
-        const bf16x8 a = kbuf[j % kKPrefetch];
-        if (j + kKPrefetch < 36) kbuf[j % kKPrefetch] = kread(j + kKPrefetch);
-        if (j & 1) s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j >> 1], s1, 0, 0, 0);
-        else s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j >> 1], s0, 0, 0, 0);
-      }
+      for (int i = 0; i < 32; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      l_run = 0.f;
+      bool overflow = false;
 
-      // V^T operands do not depend on P: start reading them before the softmax.
-      auto vread = [&](int db, int half) {
-        const int off = v_off[db & 3] + 128 * (db >> 2) + half * 16 * kRowBytes;
-        return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(T + off));
-      };
-      bf16x4 vlo[kVPrefetch], vhi[kVPrefetch];
-#pragma unroll
-      for (int j = 0; j < kVPrefetch; ++j) {
-        vlo[j] = vread(j, 0);
-        vhi[j] = vread(j, 1);
-      }
+      for (int it = 0; it < ntiles; ++it) {
+        const int ahead = ntiles - 1 - it;  // tiles issued after this one (capped below)
+        if (ahead >= kStages - 2) wait_vmcnt<kDmaPerWave * (kStages - 2)>();
+        else if (ahead == 1) wait_vmcnt<kDmaPerWave>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (it + kStages - 1 < ntiles) issue(it + kStages - 1, (it + kStages - 1) % kStages);
 
-      // ---- online softmax (log2 domain) for head c; lane holds tokens 4g+i and 16+4g+i
-      float x[8];
+        const MLA_LDS char* T = (const MLA_LDS char*)smem + (it % kStages) * kTileBytes;
+
+        // ---- S^T = K . Q^T : tokens 0-15 (s0) and 16-31 (s1) of the tile.
+        // Read j covers k-step j>>1 of token block j&1.
+        auto kread = [&](int j) {
+          const int ks = j >> 1;
+          const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (j & 1) * 16 * kRowBytes;
+          return *reinterpret_cast<const MLA_LDS bf16x8*>(T + off);
+        };
+        // kQkChains independent accumulators per token block keep the dependent
+        // MFMA chains short; they are summed after the last k-step.
+        f32x4 sacc[2][kQkChains];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = s0[i] * p.scale_log2;
-        x[4 + i] = s1[i] * p.scale_log2;
-      }
-      const int tstart = t0 + it * kTile;
-      if (tstart + kTile > t1) {
-        const int valid = t1 - tstart;
+        for (int u = 0; u < kQkChains; ++u) sacc[0][u] = sacc[1][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        bf16x8 kbuf[kKPrefetch];
+#pragma unroll
+        for (int j = 0; j < kKPrefetch; ++j) kbuf[j] = kread(j);
+#pragma unroll
+        for (int j = 0; j < 36; ++j) {
+          const bf16x8 a = kbuf[j % kKPrefetch];
+          if (j + kKPrefetch < 36) kbuf[j % kKPrefetch] = kread(j + kKPrefetch);
+          f32x4& acc = sacc[j & 1][(j >> 1) % kQkChains];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j >> 1], acc, 0, 0, 0);
+        }
+        f32x4 s0 = sacc[0][0], s1 = sacc[1][0];
+#pragma unroll
+        for (int u = 1; u < kQkChains; ++u) {
+          s0 += sacc[0][u];
+          s1 += sacc[1][u];
+        }
+
+        // V^T operands do not depend on P: start reading them before the softmax.
+        auto vread = [&](int db, int half) {
+          const int off = v_off[db & 3] + 128 * (db >> 2) + half * 16 * kRowBytes;
+          return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(T + off));
+        };
+        bf16x4 vlo[kVPrefetch], vhi[kVPrefetch];
+#pragma unroll
+        for (int j = 0; j < kVPrefetch; ++j) {
+          vlo[j] = vread(j, 0);
+          vhi[j] = vread(j, 1);
+        }
+
+        // ---- softmax numerators (log2 domain) for head c; lane holds tokens 4g+i and 16+4g+i
+        float x[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (4 * g + i >= valid) x[i] = -INFINITY;
-          if (16 + 4 * g + i >= valid) x[4 + i] = -INFINITY;
+          x[i] = s0[i] * p.scale_log2;
+          x[4 + i] = s1[i] * p.scale_log2;
         }
-      }
-      float mt = x[0];
+        const int tstart = t0 + it * kTile;
+        if (tstart + kTile > t1) {
+          const int valid = t1 - tstart;
 #pragma unroll
-      for (int i = 1; i < 8; ++i) mt = fmaxf(mt, x[i]);
-      mt = wave_max_g(mt);
-      if (it == 0) {
-        m_run = mt;  // O and l are still zero
-      } else if (__any(mt > m_run + kRescaleLog2)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
+          for (int i = 0; i < 4; ++i) {
+            if (4 * g + i >= valid) x[i] = -INFINITY;
+            if (16 + 4 * g + i >= valid) x[4 + i] = -INFINITY;
+          }
+        }
+        float mt = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        mt = wave_max_g(mt);
+        if (attempt == 0 && it == 0) m_ref = mt;
+        m_max = fmaxf(m_max, mt);
+        overflow |= mt > m_ref + kOverflowLog2;
+        float pr[8];
 #pragma unroll
-        for (int db = 0; db < 32; ++db) O[db] = O[db] * alpha;
-        m_run = m_new;
-      }
-      float pr[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
-        l_run += pr[i];
-      }
-      u32x4 pw;
-      pw[0] = pack_bf16x2(pr[0], pr[1]);
-      pw[1] = pack_bf16x2(pr[2], pr[3]);
-      pw[2] = pack_bf16x2(pr[4], pr[5]);
-      pw[3] = pack_bf16x2(pr[6], pr[7]);
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+        for (int i = 0; i < 8; ++i) {
+          pr[i] = __builtin_amdgcn_exp2f(x[i] - m_ref);
+          l_run += pr[i];
+        }
+        u32x4 pw;
+        pw[0] = pack_bf16x2(pr[0], pr[1]);
+        pw[1] = pack_bf16x2(pr[2], pr[3]);
+        pw[2] = pack_bf16x2(pr[4], pr[5]);
+        pw[3] = pack_bf16x2(pr[6], pr[7]);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
 
-      // ---- O^T += V^T . P^T over 32 blocks of 16 dims
+        // ---- O^T += V^T . P^T over 32 blocks of 16 dims
 #pragma unroll
-      for (int db = 0; db < 32; ++db) {
-        const bf16x8 a =
-            __builtin_shufflevector(vlo[db % kVPrefetch], vhi[db % kVPrefetch], 0, 1, 2, 3, 4, 5, 6, 7);
-        if (db + kVPrefetch < 32) {
-          vlo[db % kVPrefetch] = vread(db + kVPrefetch, 0);
-          vhi[db % kVPrefetch] = vread(db + kVPrefetch, 1);
+        for (int db = 0; db < 32; ++db) {
+          const bf16x8 a =
+              __builtin_shufflevector(vlo[db % kVPrefetch], vhi[db % kVPrefetch], 0, 1, 2, 3, 4, 5, 6, 7);
+          if (db + kVPrefetch < 32) {
+            vlo[db % kVPrefetch] = vread(db + kVPrefetch, 0);
+            vhi[db % kVPrefetch] = vread(db + kVPrefetch, 1);
+          }
+          O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, O[db], 0, 0, 0);
         }
-        O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, O[db], 0, 0, 0);
+      }
+      // every wave has drained its loads (vmcnt(0) at the last tile); agree on a re-run
+      if (attempt == 0) {
+        if (!__syncthreads_or(overflow)) break;
+        m_ref = m_max;  // exact max of the piece: exp2(x - m_ref) <= 1 everywhere
       }
     }
 
     // ---- finalise: lane holds head h, dims 16*db + 4g + (0..3)
     const float l_tot = wave_sum_g(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const float lse_nat = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    const float lse_nat = l_tot > 0.f ? (m_ref + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
     if (npieces == 1) {
       __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 4 * g;
 #pragma unroll
@@ -369,6 +354,7 @@ hipError_t launch_decode_nw(const DecodeParams& p, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  if (p.heads == 64 && p.log2_ps >= 5) return launch_decode_stream(p, stream);
   switch (p.heads / 16) {
     case 1: return launch_decode_nw<1>(p, stream);
     case 2: return launch_decode_nw<2>(p, stream);

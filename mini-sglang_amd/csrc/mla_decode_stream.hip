@@ -1,0 +1,405 @@
+// Streaming absorbed-MLA decode for 64 query heads and pages of >= 32 tokens
+// (the Kimi-K2 / DeepSeek-V3 decode shape on one GPU).
+//
+// Same plan, workspace and outputs as mla_decode_kernel, different schedule:
+//  * The CTA's whole (request, token) range is ONE stream of 32-token tiles:
+//    the 4-stage LDS ring keeps prefetching across piece boundaries, so a new
+//    piece costs one query load instead of a drained-and-refilled ring.
+//  * 4 waves = 2 head groups (32 heads) x 2 value halves (256 dims). Each wave
+//    computes S for its 32 heads (every 16-byte K read feeds two MFMAs) and
+//    O for its 256 value dims (every transposing V read feeds two MFMAs).
+//  * Page ids and sequence lengths are read with scalar loads, and barriers
+//    wait on LDS only, so the only vector-memory operations in flight are the
+//    ring's DMA loads and the output stores, both counted explicitly.
+#include "mla_common.h"
+#include "mla_device.h"
+
+namespace mla {
+namespace {
+
+constexpr int kSWaves = 4;
+constexpr int kSDma = kTileDma / kSWaves;  // DMA loads per wave per tile (9)
+constexpr int kSKPrefetch = 6;             // K operands in flight
+constexpr int kSVPrefetch = 4;             // V operand pairs in flight
+constexpr float kSOverflowLog2 = 64.0f;    // see mla_decode.hip
+
+// Position in the CTA's stream: request rb + b, tile start t, piece [t0, t1).
+struct Cursor {
+  int b, t, t0, t1;
+};
+
+__global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * kTileBytes];
+  __shared__ int s_flag[kSWaves];
+  // the CTA's range, staged once: per request r (= b - rb) its piece [t0, t1),
+  // first stream tile, pieces and partial-slot offset; per stream tile its page id
+  __shared__ int s_t0[kMaxCtaRequests], s_t1[kMaxCtaRequests], s_tbase[kMaxCtaRequests + 1];
+  __shared__ int s_np[kMaxCtaRequests], s_slot0[kMaxCtaRequests];
+  __shared__ int s_pid[2 * kMaxCtaBlocks];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hg = wave & 1;   // heads 32*hg .. +32 (two 16-head blocks)
+  const int dh = wave >> 1;  // value dims 256*dh .. +256
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int w = blockIdx.x;
+
+  int rb, kb, re, ke;
+  sload_i32x4(p.plan + 4 * w, rb, kb, re, ke);
+  const int ps_mask = (1 << p.log2_ps) - 1;
+  const int row_bytes = (int)(p.kv_row_stride * 2);
+  const char* kv = reinterpret_cast<const char*>(p.kv);
+  const uint32_t lds_ring = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
+
+  // ---- per-lane LDS read offsets (bytes within a tile)
+  const int xk = swz(c & 7);
+  const int k_off_even = c * kRowBytes + ((g ^ xk) << 4);
+  const int k_off_odd = c * kRowBytes + (((4 + g) ^ xk) << 4);
+  int v_off[4];  // this wave's value half starts 512 bytes into the row (before swizzle groups)
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    v_off[q4] = (4 * g + (c >> 2)) * kRowBytes + 512 * dh +
+                ((2 * (q4 ^ (c >> 2)) + (((c & 3) >> 1) ^ (g & 1))) << 4) + ((c & 1) << 3);
+  uint32_t dma_voff[kSDma];
+#pragma unroll
+  for (int k = 0; k < kSDma; ++k) {
+    const int s = (wave + k * kSWaves) * 64 + lane;
+    const int t = (s * 7282) >> 19;  // s / 72 for s < 2304
+    dma_voff[k] = t * row_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4);
+  }
+
+  // ---- stage the range: request bounds, then one page id per 32-token tile
+  int rlast = (ke == 0 ? re - 1 : re);
+  rlast = min(rlast, p.batch - 1);
+  const int nreq = min(rlast - rb + 1, kMaxCtaRequests);
+  if (nreq <= 0) return;  // uniform: an empty range
+  for (int r = threadIdx.x; r < nreq; r += 256) {
+    const int b = rb + r;
+    const int L = p.seq_lens[b];
+    const int t0 = (r == 0) ? kb * kPlanBlock : 0;
+    const int t1 = max(t0, (b == re) ? min(ke * kPlanBlock, L) : L);
+    s_t0[r] = t0;
+    s_t1[r] = t1;
+    s_tbase[r + 1] = (t1 - t0 + kTile - 1) / kTile;
+    const int first = p.plan[4 * p.num_ctas + 3 * b + 0];
+    s_np[r] = p.plan[4 * p.num_ctas + 3 * b + 1];
+    s_slot0[r] = p.plan[4 * p.num_ctas + 3 * b + 2] - first;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive prefix of tile counts (nreq <= 256: four 64-wide scans)
+    int carry = 0;
+    for (int c0 = 0; c0 < nreq; c0 += 64) {
+      const int r = c0 + lane;
+      int v = r < nreq ? s_tbase[r + 1] : 0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+      }
+      if (r < nreq) s_tbase[r + 1] = carry + v;
+      carry += __shfl(v, 63);
+    }
+    if (lane == 0) s_tbase[0] = 0;
+  }
+  __syncthreads();
+  const int ntiles_cta = min(s_tbase[nreq], 2 * kMaxCtaBlocks);
+  {
+    constexpr int kPer = 2 * kMaxCtaBlocks / 256;
+    int pid[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = threadIdx.x + 256 * u;
+      pid[u] = 0;
+      if (k < ntiles_cta) {
+        int lo = 0, hi = nreq - 1;  // last request whose first tile is <= k
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_tbase[mid] <= k) lo = mid;
+          else hi = mid - 1;
+        }
+        const int t = s_t0[lo] + kTile * (k - s_tbase[lo]);
+        pid[u] = p.page_table[(int64_t)(rb + lo) * p.pt_stride + (t >> p.log2_ps)];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = threadIdx.x + 256 * u;
+      if (k < ntiles_cta) s_pid[k] = min(max(pid[u], 0), p.num_pages - 1);
+    }
+  }
+  __syncthreads();
+
+  // ---- stream cursors over (request, tile); all values wave-uniform
+  auto seek = [&](Cursor& cur, int r) -> bool {  // first non-empty piece at or after request rb + r
+    for (; r < nreq; ++r) {
+      const int t0 = __builtin_amdgcn_readfirstlane(s_t0[r]);
+      const int t1 = __builtin_amdgcn_readfirstlane(s_t1[r]);
+      if (t1 > t0) {
+        cur = Cursor{r, t0, t0, t1};
+        return true;
+      }
+    }
+    return false;
+  };
+  auto advance = [&](Cursor& cur) -> bool {
+    cur.t += kTile;
+    return cur.t < cur.t1 ? true : seek(cur, cur.b + 1);
+  };
+  auto issue = [&](const Cursor& cur, int n) {  // DMA stream tile n (at cur) into ring stage n % kStages
+    const int pid = __builtin_amdgcn_readfirstlane(s_pid[min(n, 2 * kMaxCtaBlocks - 1)]);
+    const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (cur.t & ps_mask)) * row_bytes;
+    const uint32_t lds_stage = lds_ring + (n % kStages) * kTileBytes;
+    const int tlim = cur.t1 - 1 - cur.t;  // loads clamp to the piece's last token
+    if (tlim >= kTile - 1) {
+#pragma unroll
+      for (int k = 0; k < kSDma; ++k) dma16_saddr(tsrc, dma_voff[k], lds_stage + (wave + k * kSWaves) * 1024);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kSDma; ++k) {
+        const int s = (wave + k * kSWaves) * 64 + lane;
+        const int t = (s * 7282) >> 19;
+        const uint32_t voff = min(t, tlim) * row_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4);
+        dma16_saddr(tsrc, voff, lds_stage + (wave + k * kSWaves) * 1024);
+      }
+    }
+  };
+
+  Cursor comp;
+  if (!seek(comp, 0)) return;  // uniform: every piece of the range is empty
+  Cursor iss = comp;
+
+  // ---- queries of the current piece: qf[hb][ks] = head 32hg+16hb+c, dims 32ks + 8g .. +8
+  bf16x8 qf[2][18];
+  auto load_q = [&](int b) {
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const __bf16* qrow =
+          p.q + (int64_t)b * p.q_stride_b + (int64_t)(32 * hg + 16 * hb + c) * p.q_stride_h + g * 8;
+#pragma unroll
+      for (int ks = 0; ks < 18; ++ks) qf[hb][ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
+    }
+    // consume: the compiler's wait for these loads lands here, outside the tile loop
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int ks = 0; ks < 18; ++ks) asm volatile("" ::"v"(qf[hb][ks]));
+  };
+  load_q(rb + comp.b);
+
+  int n_issued = 0;
+  bool iss_valid = true;
+  auto prologue = [&]() {
+    for (int s = 0; s < kStages - 1 && iss_valid; ++s) {
+      issue(iss, n_issued++);
+      iss_valid = advance(iss);
+    }
+  };
+  prologue();
+
+  // ---- piece state
+  f32x4 O[2][16];
+  float m_ref[2] = {0.f, 0.f}, m_max[2], l_run[2];
+  bool overflow = false;
+  int attempt = 0;
+  bool piece_start = true, need_q = false;
+  Cursor piece_cur = comp;
+  int piece_j = 0;
+  int st1 = 0, st2 = 0, st3 = 0;  // output stores issued 1, 2 and 3 iterations ago
+
+  for (int j = 0;;) {
+    // tile j's DMA is complete once at most (loads issued after it + stores since) remain
+    wait_vmcnt_dyn(kSDma * (n_issued - 1 - j) + st1 + st2 + st3);
+    barrier_lds();
+    st3 = st2;
+    st2 = st1;
+    st1 = 0;
+    if (need_q) {  // first tile of a new piece: its queries (waited for right here)
+      load_q(rb + comp.b);
+      need_q = false;
+    }
+    if (iss_valid) {
+      issue(iss, n_issued++);
+      iss_valid = advance(iss);
+    }
+    if (piece_start) {
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+#pragma unroll
+        for (int db = 0; db < 16; ++db) O[hb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        l_run[hb] = 0.f;
+        m_max[hb] = -INFINITY;
+      }
+      overflow = false;
+    }
+
+    const MLA_LDS char* T = (const MLA_LDS char*)smem + (j % kStages) * kTileBytes;
+
+    // ---- S^T[token block tb][head block hb] = K . Q^T
+    auto kread = [&](int r) {  // read r: k-step r>>1 of token block r&1
+      const int ks = r >> 1;
+      const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (r & 1) * 16 * kRowBytes;
+      return *reinterpret_cast<const MLA_LDS bf16x8*>(T + off);
+    };
+    f32x4 sacc[2][2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) sacc[tb][0] = sacc[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 kbuf[kSKPrefetch];
+#pragma unroll
+    for (int r = 0; r < kSKPrefetch; ++r) kbuf[r] = kread(r);
+#pragma unroll
+    for (int r = 0; r < 36; ++r) {
+      const bf16x8 a = kbuf[r % kSKPrefetch];
+      if (r + kSKPrefetch < 36) kbuf[r % kSKPrefetch] = kread(r + kSKPrefetch);
+      const int tb = r & 1, ks = r >> 1;
+      sacc[tb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], sacc[tb][0], 0, 0, 0);
+      sacc[tb][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], sacc[tb][1], 0, 0, 0);
+    }
+
+    auto vread = [&](int db, int half) {
+      const int off = v_off[db & 3] + 128 * (db >> 2) + half * 16 * kRowBytes;
+      return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(T + off));
+    };
+    bf16x4 vlo[kSVPrefetch], vhi[kSVPrefetch];
+#pragma unroll
+    for (int r = 0; r < kSVPrefetch; ++r) {
+      vlo[r] = vread(r, 0);
+      vhi[r] = vread(r, 1);
+    }
+
+    // ---- softmax numerators per head block; lane holds tokens 4g+i (tb 0) and 16+4g+i (tb 1)
+    const int valid = comp.t1 - comp.t;  // tokens of this tile inside the piece
+    bf16x8 pb[2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = sacc[0][hb][i] * p.scale_log2;
+        x[4 + i] = sacc[1][hb][i] * p.scale_log2;
+      }
+      if (valid < kTile) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (4 * g + i >= valid) x[i] = -INFINITY;
+          if (16 + 4 * g + i >= valid) x[4 + i] = -INFINITY;
+        }
+      }
+      float mt = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      mt = wave_max_g(mt);
+      if (piece_start && attempt == 0) m_ref[hb] = mt;
+      m_max[hb] = fmaxf(m_max[hb], mt);
+      overflow |= mt > m_ref[hb] + kSOverflowLog2;
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(x[i] - m_ref[hb]);
+        l_run[hb] += pr[i];
+      }
+      u32x4 pw;
+      pw[0] = pack_bf16x2(pr[0], pr[1]);
+      pw[1] = pack_bf16x2(pr[2], pr[3]);
+      pw[2] = pack_bf16x2(pr[4], pr[5]);
+      pw[3] = pack_bf16x2(pr[6], pr[7]);
+      pb[hb] = __builtin_bit_cast(bf16x8, pw);
+    }
+
+    // ---- O^T[16 dims x 16 heads] += V^T . P^T for this wave's 16 dim blocks, both head blocks
+#pragma unroll
+    for (int db = 0; db < 16; ++db) {
+      const bf16x8 a =
+          __builtin_shufflevector(vlo[db % kSVPrefetch], vhi[db % kSVPrefetch], 0, 1, 2, 3, 4, 5, 6, 7);
+      if (db + kSVPrefetch < 16) {
+        vlo[db % kSVPrefetch] = vread(db + kSVPrefetch, 0);
+        vhi[db % kSVPrefetch] = vread(db + kSVPrefetch, 1);
+      }
+      O[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0], O[0][db], 0, 0, 0);
+      O[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1], O[1][db], 0, 0, 0);
+    }
+
+    const bool piece_end = comp.t + kTile >= comp.t1;
+    piece_start = false;
+    if (piece_end) {
+      // CTA-wide: did any head of the piece overflow its exponent reference?
+      if (lane == 0) s_flag[wave] = overflow ? 1 : 0;
+      barrier_lds();
+      const bool any_overflow = (s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3]) != 0;
+      if (any_overflow && attempt == 0) {
+        // rare: rewind the stream to the piece start and rerun it with the exact max
+        wait_vmcnt<0>();
+        barrier_lds();
+        comp = piece_cur;
+        iss = piece_cur;
+        j = piece_j;
+        n_issued = piece_j;
+        iss_valid = true;
+        st1 = st2 = st3 = 0;
+        m_ref[0] = m_max[0];
+        m_ref[1] = m_max[1];
+        attempt = 1;
+        piece_start = true;
+        prologue();
+        continue;
+      }
+      attempt = 0;
+
+      // ---- finalise: lane holds heads 32hg+16hb+c, dims 256dh + 16db + 4g + (0..3)
+      const int b = rb + comp.b;
+      const int npieces = __builtin_amdgcn_readfirstlane(s_np[comp.b]);
+      int stores = 0;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const int h = 32 * hg + 16 * hb + c;
+        const float l_tot = wave_sum_g(l_run[hb]);
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        const float lse_nat = l_tot > 0.f ? (m_ref[hb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+        if (npieces == 1) {
+          __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 256 * dh + 4 * g;
+#pragma unroll
+          for (int db = 0; db < 16; ++db) {
+            u32x2 v;
+            v[0] = pack_bf16x2(O[hb][db][0] * inv, O[hb][db][1] * inv);
+            v[1] = pack_bf16x2(O[hb][db][2] * inv, O[hb][db][3] * inv);
+            *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+          }
+          stores += 16;
+          if (p.lse != nullptr && dh == 0) {
+            if (g == 0) p.lse[(int64_t)b * p.lse_stride_b + h] = lse_nat;
+            stores += 1;
+          }
+        } else {
+          const int slot = __builtin_amdgcn_readfirstlane(s_slot0[comp.b]) + w;
+          if (slot >= 0 && slot < p.ws_slots) {
+            float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * dh + 4 * g;
+#pragma unroll
+            for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[hb][db] * inv;
+            stores += 16;
+            if (dh == 0) {
+              if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
+              stores += 1;
+            }
+          }
+        }
+      }
+      st1 = stores;
+    }
+
+    ++j;
+    if (!advance(comp)) break;
+    if (piece_end) {
+      piece_start = true;
+      need_q = true;
+      piece_cur = comp;
+      piece_j = j;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode_stream(const DecodeParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(mla_decode_stream_kernel, dim3(p.num_ctas), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace mla

@@ -1,0 +1,93 @@
+// Device helpers shared by the gfx950 MLA decode kernels.
+#pragma once
+
+#include "mla_common.h"
+
+namespace mla {
+
+// Row swizzle of the LDS tiles: 16-byte chunk c of token t is stored at chunk
+// position c ^ swz(t & 7).
+__device__ __forceinline__ int swz(int t7) { return ((t7 & 3) << 1) | ((t7 >> 2) & 1); }
+
+__device__ __forceinline__ float wave_max_g(float v) {
+  // reduce over the 4 lane groups (lanes l, l^16, l^32, l^48)
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_g(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+// The counter saturates at 63; a smaller count only waits longer, so N is clamped.
+template <int N0>
+__device__ __forceinline__ void wait_vmcnt() {
+  constexpr int N = N0 > 63 ? 63 : N0;
+  static_assert(N >= 0, "vmcnt range");
+  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4]=7 | lgkmcnt[11:8]=15 | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+
+// 16-byte global -> LDS DMA; lane i's data lands at LDS byte address
+// lds_base + 16*i. Issued as inline asm so that the compiler's wait-count
+// pass does not serialise later LDS reads of other stages behind it: every
+// read of a staged tile is preceded by wait_vmcnt + a workgroup barrier.
+__device__ __forceinline__ void dma16_saddr(const char* base, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  // round-to-nearest-even, matching torch's float->bfloat16 conversion
+  __bf16 x = (__bf16)a, y = (__bf16)b;
+  uint16_t ux = __builtin_bit_cast(uint16_t, x), uy = __builtin_bit_cast(uint16_t, y);
+  return (uint32_t)ux | ((uint32_t)uy << 16);
+}
+
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS ops, then
+// s_barrier. Unlike __syncthreads() it never waits on vector-memory counters,
+// so in-flight DMA loads and output stores stay in flight.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Scalar (wave-uniform) 32-bit load, waited for before returning.
+__device__ __forceinline__ int sload_i32(const int32_t* ptr) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr) : "memory");
+  return v;
+}
+
+// Scalar load of four consecutive 32-bit values (16-byte aligned), waited for.
+__device__ __forceinline__ void sload_i32x4(const int32_t* ptr, int& a, int& b, int& c, int& d) {
+  typedef int i32x4_t __attribute__((__vector_size__(16)));
+  i32x4_t v;
+  asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr) : "memory");
+  a = v[0];
+  b = v[1];
+  c = v[2];
+  d = v[3];
+}
+
+// wait_vmcnt with a run-time (wave-uniform) count, clamped to the counter range.
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  n = n > 63 ? 63 : (n < 0 ? 0 : n);
+  switch (n) {
+#define MLA_VM_CASE(k) \
+  case k:              \
+    wait_vmcnt<k>();   \
+    break;
+#define MLA_VM_CASE8(k) MLA_VM_CASE(k) MLA_VM_CASE(k + 1) MLA_VM_CASE(k + 2) MLA_VM_CASE(k + 3) \
+    MLA_VM_CASE(k + 4) MLA_VM_CASE(k + 5) MLA_VM_CASE(k + 6) MLA_VM_CASE(k + 7)
+    MLA_VM_CASE8(0) MLA_VM_CASE8(8) MLA_VM_CASE8(16) MLA_VM_CASE8(24)
+    MLA_VM_CASE8(32) MLA_VM_CASE8(40) MLA_VM_CASE8(48) MLA_VM_CASE8(56)
+#undef MLA_VM_CASE8
+#undef MLA_VM_CASE
+  }
+}
+
+}  // namespace mla

@@ -38,10 +38,17 @@ SIGNATURES = {
         [_vp, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i32,
          _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp],
     ),
-    "mla_decode_merge_f32": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "mla_decode_split_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i32,
+         _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
+    "mla_decode_merge_f32": (
+        ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _vp]
+    ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -159,9 +166,13 @@ def decode_plan(
 
 def mla_decode(
     q, kv_pool, page_table, seq_lens, plan, num_ctas: int, ws_o, ws_lse, scale: float, out, lse=None,
-    stream=None,
+    stream=None, split_only: bool = False,
 ) -> None:
-    """Absorbed-MLA decode: ``q [B, H, 576]``, ``kv_pool [pages, ps, 576]`` -> ``out [B, H, 512]``."""
+    """Absorbed-MLA decode: ``q [B, H, 576]``, ``kv_pool [pages, ps, 576]`` -> ``out [B, H, 512]``.
+
+    ``split_only`` launches just the split kernel (partials stay in the
+    workspace for ``mla_decode_merge(..., single_piece_final=True)``).
+    """
     import torch
 
     B, H, D = q.shape
@@ -177,23 +188,25 @@ def mla_decode(
         assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32
     if lse is not None:
         assert lse.dtype == torch.float32 and lse.shape == (B, H) and lse.stride(-1) == 1
+    fn = load_library().mla_decode_split_bf16 if split_only else load_library().mla_decode_bf16
     check(
-        load_library().mla_decode_bf16(
+        fn(
             _ptr(q), q.stride(0), q.stride(1), _ptr(kv_pool), kv_pool.stride(1),
             kv_pool.shape[0], kv_pool.shape[1], _ptr(page_table), page_table.stride(0), _ptr(seq_lens), B, H,
             float(scale), _ptr(plan), num_ctas, _ptr(ws_o), _ptr(ws_lse), ws_slots, _ptr(out), out.stride(0),
             out.stride(1), _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
         ),
-        "mla_decode_bf16",
+        "mla_decode_split_bf16" if split_only else "mla_decode_bf16",
     )
 
 
-def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None) -> None:
+def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None, single_piece_final: bool = False) -> None:
     """fp32 LSE merge of partials ``ws_o [S, H, 512]`` / ``ws_lse [S, H]`` per ``req_info``."""
     B, H = out.shape[0], out.shape[1]
     check(
         load_library().mla_decode_merge_f32(
-            _ptr(ws_o), _ptr(ws_lse), ws_o.shape[0], _ptr(req_info), B, H, _ptr(out), out.stride(0), out.stride(1),
+            _ptr(ws_o), _ptr(ws_lse), ws_o.shape[0], _ptr(req_info), B, H, int(single_piece_final), _ptr(out),
+            out.stride(0), out.stride(1),
             _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
         ),
         "mla_decode_merge_f32",

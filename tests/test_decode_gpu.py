@@ -94,15 +94,23 @@ def test_decode_golden_fixture():
         torch.testing.assert_close(lse.double(), torch.from_numpy(f["lse"]), **LSE_TOL)
 
 
-def test_decode_large_logits_rescale():
-    """Scores that grow along the sequence force the softmax rescale path."""
-    case = make_decode_case(2, 16, 64, lens=[900, 2000], seed=9)
-    ramp = torch.linspace(0, 30, case.kv_pool.shape[0] * 64).view(-1, 64, 1)
+@pytest.mark.parametrize("heads,top", [(16, 30.0), (16, 90.0), (64, 90.0)])
+def test_decode_large_logits(heads, top):
+    """Scores that grow along the sequence by more than 2^64 force the exact-max rerun of a piece."""
+    case = make_decode_case(2, heads, 64, lens=[900, 2000], seed=9)
+    ramp = torch.linspace(0, top, case.kv_pool.shape[0] * 64).view(-1, 64, 1)
     kv = case.kv_pool.float()
     kv[..., 512:513] = ramp  # rope column grows with the flat row index
     case.kv_pool = kv.to(torch.bfloat16)
     case.q[..., 512] = 20.0
     check_case(case, 8)
+
+
+@pytest.mark.parametrize("ps,num_ctas", [(32, 256), (128, 256), (64, 3), (32, 40)])
+def test_decode_64_heads_page_sizes(ps, num_ctas):
+    """64 heads with pages of >= 32 tokens (the streaming kernel), ragged lengths, many pieces per CTA."""
+    case = make_decode_case(9, 64, ps, lens=[1, 33, 64, 96, 130, 255, 1000, 2049, 31], seed=ps)
+    check_case(case, num_ctas)
 
 
 def test_merge_kernel_standalone():
@@ -155,3 +163,24 @@ def test_page_table_kernel_bit_exact():
         got = lib.page_table_from_tokens(tt.to(DEV), idx.to(DEV), 4000, ps)
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), ref)
+
+
+def test_split_then_merge_equals_one_call():
+    """mla_decode_split_bf16 + mla_decode_merge_f32(single_piece_final) == mla_decode_bf16, bit for bit."""
+    case = make_decode_case(6, 64, 64, lens=[5000, 70, 1, 3000, 129, 640], seed=11)
+    q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
+    plan_np, slots = lib.decode_plan(case.lens, 64, 32)
+    plan = torch.from_numpy(plan_np).to(DEV)
+    ws_o = torch.empty((max(slots, 1), 64, 512), dtype=torch.float32, device=DEV)
+    ws_lse = torch.empty((max(slots, 1), 64), dtype=torch.float32, device=DEV)
+    outs = []
+    for two_step in (False, True):
+        out = torch.empty((6, 64, 512), dtype=torch.bfloat16, device=DEV)
+        lse = torch.empty((6, 64), dtype=torch.float32, device=DEV)
+        lib.mla_decode(q, kv, pt, sl, plan, 32, ws_o, ws_lse, R.DEFAULT_SCALE, out, lse, split_only=two_step)
+        if two_step:
+            lib.mla_decode_merge(ws_o, ws_lse, plan[32 * 4 :], out, lse, single_piece_final=True)
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), lse.cpu()))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1], outs[1][1])
