@@ -41,6 +41,9 @@ enum {
 /* Entries per CTA in a decode plan's cta_ranges and per request in req_info. */
 #define MLA_PLAN_CTA_INTS 4
 #define MLA_PLAN_REQ_INTS 3
+/* A decode plan gives one CTA at most this many plan blocks and requests. */
+#define MLA_PLAN_MAX_CTA_BLOCKS 1024
+#define MLA_PLAN_MAX_CTA_REQUESTS 128
 
 /* Message for the last failed call on this thread ("" if none). */
 const char *mla_last_error(void);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/mla_amd.h"
+
 namespace mla {
 
 typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
@@ -29,8 +31,8 @@ constexpr int kPlanBlock = 64;                 // tokens per plan block
 constexpr int kMaxPieceIds = 1024;             // page ids of one piece staged in LDS
 // Per-CTA limits of a decode plan: the streaming kernel stages one page id per
 // 32-token tile (2 per plan block) and the bounds of every request of its range.
-constexpr int kMaxCtaBlocks = 1024;
-constexpr int kMaxCtaRequests = 128;
+constexpr int kMaxCtaBlocks = MLA_PLAN_MAX_CTA_BLOCKS;
+constexpr int kMaxCtaRequests = MLA_PLAN_MAX_CTA_REQUESTS;
 
 struct DecodeParams {
   const __bf16* q;  // [B, H, 576]

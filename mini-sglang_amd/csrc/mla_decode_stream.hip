@@ -4,13 +4,20 @@
 // Same plan, workspace and outputs as mla_decode_kernel, different schedule:
 //  * The CTA's whole (request, token) range is ONE stream of 32-token tiles:
 //    the 4-stage LDS ring keeps prefetching across piece boundaries, so a new
-//    piece costs one query load instead of a drained-and-refilled ring.
-//  * 4 waves = 2 head groups (32 heads) x 2 value halves (256 dims). Each wave
-//    computes S for its 32 heads (every 16-byte K read feeds two MFMAs) and
-//    O for its 256 value dims (every transposing V read feeds two MFMAs).
-//  * Page ids and sequence lengths are read with scalar loads, and barriers
-//    wait on LDS only, so the only vector-memory operations in flight are the
-//    ring's DMA loads and the output stores, both counted explicitly.
+//    piece costs one query load instead of a drained-and-refilled ring. The
+//    page id of every tile and the bounds of every request of the range are
+//    staged in LDS once, at CTA start.
+//  * 4 waves = 2 head groups (32 heads each) x 2 halves. Wave (hg, th):
+//      S^T[16 tokens (half th) x 32 heads] = K . Q^T     36 MFMAs, 18 K reads
+//      softmax numerators of those 16 tokens, exchanged with the partner
+//      wave (hg, 1 - th) as bf16 through LDS
+//      O^T[256 dims (half th) x 32 heads] += V^T . P^T   32 MFMAs, 32 V reads
+//    over all 32 tokens. Every staged K row is read by 2 waves and every V
+//    row half by 2 waves, and no MFMA or exponential is computed twice. The
+//    pair agrees on the exponent reference at the first tile of each piece
+//    and adds its row sums at the end of the piece.
+//  * Barriers wait on LDS only, so the vector-memory operations in flight are
+//    the ring's DMA loads and the output stores, both counted explicitly.
 #include "mla_common.h"
 #include "mla_device.h"
 
@@ -23,13 +30,16 @@ constexpr int kSKPrefetch = 6;             // K operands in flight
 constexpr int kSVPrefetch = 4;             // V operand pairs in flight
 constexpr float kSOverflowLog2 = 64.0f;    // see mla_decode.hip
 
-// Position in the CTA's stream: request rb + b, tile start t, piece [t0, t1).
+// Position in the CTA's stream: request rb + r, tile start t, piece [t0, t1).
 struct Cursor {
-  int b, t, t0, t1;
+  int r, t, t0, t1;
 };
 
 __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kStages * kTileBytes];
+  // pair exchange: softmax numerators (16 B per lane), per-head maxima and row sums
+  __shared__ __attribute__((aligned(16))) u32x4 s_xp[kSWaves][64];
+  __shared__ float s_xm[kSWaves][32];
   __shared__ int s_flag[kSWaves];
   // the CTA's range, staged once: per request r (= b - rb) its piece [t0, t1),
   // first stream tile, pieces and partial-slot offset; per stream tile its page id
@@ -39,8 +49,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hg = wave & 1;   // heads 32*hg .. +32 (two 16-head blocks)
-  const int dh = wave >> 1;  // value dims 256*dh .. +256
+  const int hg = wave & 1;   // heads 32*hg .. +32 (two 16-head blocks hb)
+  const int th = wave >> 1;  // tokens 16*th .. +16 of each tile for S; value dims 256*th .. +256 for O
+  const int partner = wave ^ 2;
   const int g = lane >> 4;
   const int c = lane & 15;
   const int w = blockIdx.x;
@@ -53,13 +64,13 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   const uint32_t lds_ring = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
 
   // ---- per-lane LDS read offsets (bytes within a tile)
-  const int xk = swz(c & 7);
-  const int k_off_even = c * kRowBytes + ((g ^ xk) << 4);
-  const int k_off_odd = c * kRowBytes + (((4 + g) ^ xk) << 4);
+  const int xk = swz(c & 7);  // token 16*th + c has the swizzle of token c
+  const int k_off_even = (16 * th + c) * kRowBytes + ((g ^ xk) << 4);
+  const int k_off_odd = (16 * th + c) * kRowBytes + (((4 + g) ^ xk) << 4);
   int v_off[4];  // this wave's value half starts 512 bytes into the row (before swizzle groups)
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
-    v_off[q4] = (4 * g + (c >> 2)) * kRowBytes + 512 * dh +
+    v_off[q4] = (4 * g + (c >> 2)) * kRowBytes + 512 * th +
                 ((2 * (q4 ^ (c >> 2)) + (((c & 3) >> 1) ^ (g & 1))) << 4) + ((c & 1) << 3);
   uint32_t dma_voff[kSDma];
 #pragma unroll
@@ -87,7 +98,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     s_slot0[r] = p.plan[4 * p.num_ctas + 3 * b + 2] - first;
   }
   __syncthreads();
-  if (wave == 0) {  // exclusive prefix of tile counts (nreq <= 256: four 64-wide scans)
+  if (wave == 0) {  // exclusive prefix of tile counts (64-wide scans)
     int carry = 0;
     for (int c0 = 0; c0 < nreq; c0 += 64) {
       const int r = c0 + lane;
@@ -144,7 +155,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   };
   auto advance = [&](Cursor& cur) -> bool {
     cur.t += kTile;
-    return cur.t < cur.t1 ? true : seek(cur, cur.b + 1);
+    return cur.t < cur.t1 ? true : seek(cur, cur.r + 1);
   };
   auto issue = [&](const Cursor& cur, int n) {  // DMA stream tile n (at cur) into ring stage n % kStages
     const int pid = __builtin_amdgcn_readfirstlane(s_pid[min(n, 2 * kMaxCtaBlocks - 1)]);
@@ -185,7 +196,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
 #pragma unroll
       for (int ks = 0; ks < 18; ++ks) asm volatile("" ::"v"(qf[hb][ks]));
   };
-  load_q(rb + comp.b);
+  load_q(rb + comp.r);
 
   int n_issued = 0;
   bool iss_valid = true;
@@ -197,7 +208,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   };
   prologue();
 
-  // ---- piece state
+  // ---- piece state; m_max and overflow are tracked per lane and reduced when needed
   f32x4 O[2][16];
   float m_ref[2] = {0.f, 0.f}, m_max[2], l_run[2];
   bool overflow = false;
@@ -215,7 +226,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     st2 = st1;
     st1 = 0;
     if (need_q) {  // first tile of a new piece: its queries (waited for right here)
-      load_q(rb + comp.b);
+      load_q(rb + comp.r);
       need_q = false;
     }
     if (iss_valid) {
@@ -227,33 +238,31 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
       for (int hb = 0; hb < 2; ++hb) {
 #pragma unroll
         for (int db = 0; db < 16; ++db) O[hb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        l_run[hb] = 0.f;
-        m_max[hb] = -INFINITY;
       }
+      l_run[0] = l_run[1] = 0.f;
+      m_max[0] = m_max[1] = -INFINITY;
       overflow = false;
     }
 
     const MLA_LDS char* T = (const MLA_LDS char*)smem + (j % kStages) * kTileBytes;
 
-    // ---- S^T[token block tb][head block hb] = K . Q^T
-    auto kread = [&](int r) {  // read r: k-step r>>1 of token block r&1
-      const int ks = r >> 1;
-      const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (r & 1) * 16 * kRowBytes;
+    // ---- S^T[16 tokens x 16 heads] per head block hb, two accumulation chains each
+    auto kread = [&](int ks) {
+      const int off = ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1);
       return *reinterpret_cast<const MLA_LDS bf16x8*>(T + off);
     };
     f32x4 sacc[2][2];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) sacc[tb][0] = sacc[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hb = 0; hb < 2; ++hb) sacc[hb][0] = sacc[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     bf16x8 kbuf[kSKPrefetch];
 #pragma unroll
     for (int r = 0; r < kSKPrefetch; ++r) kbuf[r] = kread(r);
 #pragma unroll
-    for (int r = 0; r < 36; ++r) {
-      const bf16x8 a = kbuf[r % kSKPrefetch];
-      if (r + kSKPrefetch < 36) kbuf[r % kSKPrefetch] = kread(r + kSKPrefetch);
-      const int tb = r & 1, ks = r >> 1;
-      sacc[tb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], sacc[tb][0], 0, 0, 0);
-      sacc[tb][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], sacc[tb][1], 0, 0, 0);
+    for (int ks = 0; ks < 18; ++ks) {
+      const bf16x8 a = kbuf[ks % kSKPrefetch];
+      if (ks + kSKPrefetch < 18) kbuf[ks % kSKPrefetch] = kread(ks + kSKPrefetch);
+      sacc[0][ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], sacc[0][ks & 1], 0, 0, 0);
+      sacc[1][ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], sacc[1][ks & 1], 0, 0, 0);
     }
 
     auto vread = [&](int db, int half) {
@@ -267,44 +276,58 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
       vhi[r] = vread(r, 1);
     }
 
-    // ---- softmax numerators per head block; lane holds tokens 4g+i (tb 0) and 16+4g+i (tb 1)
+    // ---- softmax numerators of this wave's tokens: lane (g, c) holds tokens 16th + 4g + i of head c
     const int valid = comp.t1 - comp.t;  // tokens of this tile inside the piece
-    bf16x8 pb[2];
+    float x[2][4], mt[2];                // mt: this lane's max over its 4 tokens
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
-      float x[8];
+      const f32x4 sv = sacc[hb][0] + sacc[hb][1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[i] = sacc[0][hb][i] * p.scale_log2;
-        x[4 + i] = sacc[1][hb][i] * p.scale_log2;
+        x[hb][i] = sv[i] * p.scale_log2;
+        if (valid < kTile && 16 * th + 4 * g + i >= valid) x[hb][i] = -INFINITY;
       }
-      if (valid < kTile) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (4 * g + i >= valid) x[i] = -INFINITY;
-          if (16 + 4 * g + i >= valid) x[4 + i] = -INFINITY;
-        }
+      mt[hb] = fmaxf(fmaxf(x[hb][0], x[hb][1]), fmaxf(x[hb][2], x[hb][3]));
+    }
+    if (piece_start && attempt == 0) {
+      // exponent reference: max over the first tile's 32 tokens, agreed with the partner
+      const float w0 = wave_max_g(mt[0]), w1 = wave_max_g(mt[1]);
+      if (g == 0) {
+        s_xm[wave][c] = w0;
+        s_xm[wave][16 + c] = w1;
       }
-      float mt = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-      mt = wave_max_g(mt);
-      if (piece_start && attempt == 0) m_ref[hb] = mt;
-      m_max[hb] = fmaxf(m_max[hb], mt);
-      overflow |= mt > m_ref[hb] + kSOverflowLog2;
-      float pr[8];
+      barrier_lds();
+      m_ref[0] = fmaxf(w0, s_xm[partner][c]);
+      m_ref[1] = fmaxf(w1, s_xm[partner][16 + c]);
+    }
+    u32x2 pown[2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(x[i] - m_ref[hb]);
+    for (int hb = 0; hb < 2; ++hb) {
+      m_max[hb] = fmaxf(m_max[hb], mt[hb]);
+      overflow |= mt[hb] > m_ref[hb] + kSOverflowLog2;
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(x[hb][i] - m_ref[hb]);
         l_run[hb] += pr[i];
       }
-      u32x4 pw;
-      pw[0] = pack_bf16x2(pr[0], pr[1]);
-      pw[1] = pack_bf16x2(pr[2], pr[3]);
-      pw[2] = pack_bf16x2(pr[4], pr[5]);
-      pw[3] = pack_bf16x2(pr[6], pr[7]);
-      pb[hb] = __builtin_bit_cast(bf16x8, pw);
+      pown[hb][0] = pack_bf16x2(pr[0], pr[1]);
+      pown[hb][1] = pack_bf16x2(pr[2], pr[3]);
+    }
+    // P^T B operand of lane (g, c): k = 8g + i is token 4g + i (i < 4, half 0) or 16 + 4g + i - 4 (half 1)
+    s_xp[wave][lane] = u32x4{pown[0][0], pown[0][1], pown[1][0], pown[1][1]};
+    barrier_lds();
+    const u32x4 pp = s_xp[partner][lane];
+    bf16x8 pb[2];
+    if (th == 0) {
+      pb[0] = __builtin_bit_cast(bf16x8, (u32x4{pown[0][0], pown[0][1], pp[0], pp[1]}));
+      pb[1] = __builtin_bit_cast(bf16x8, (u32x4{pown[1][0], pown[1][1], pp[2], pp[3]}));
+    } else {
+      pb[0] = __builtin_bit_cast(bf16x8, (u32x4{pp[0], pp[1], pown[0][0], pown[0][1]}));
+      pb[1] = __builtin_bit_cast(bf16x8, (u32x4{pp[2], pp[3], pown[1][0], pown[1][1]}));
     }
 
-    // ---- O^T[16 dims x 16 heads] += V^T . P^T for this wave's 16 dim blocks, both head blocks
+    // ---- O^T[16 dims x 16 heads] += V^T . P^T: this wave's 16 dim blocks, both head blocks
 #pragma unroll
     for (int db = 0; db < 16; ++db) {
       const bf16x8 a =
@@ -320,41 +343,54 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     const bool piece_end = comp.t + kTile >= comp.t1;
     piece_start = false;
     if (piece_end) {
-      // CTA-wide: did any head of the piece overflow its exponent reference?
-      if (lane == 0) s_flag[wave] = overflow ? 1 : 0;
+      // CTA-wide overflow vote; the row sums of the pair travel with it
+      const float lw0 = wave_sum_g(l_run[0]), lw1 = wave_sum_g(l_run[1]);
+      if (g == 0) {
+        s_xm[wave][c] = lw0;
+        s_xm[wave][16 + c] = lw1;
+      }
+      const bool wave_overflow = __ballot(overflow) != 0;
+      if (lane == 0) s_flag[wave] = wave_overflow ? 1 : 0;
       barrier_lds();
       const bool any_overflow = (s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3]) != 0;
       if (any_overflow && attempt == 0) {
-        // rare: rewind the stream to the piece start and rerun it with the exact max
+        // rare: rewind the stream to the piece start and rerun it with the exact max of the pair
         wait_vmcnt<0>();
         barrier_lds();
+        const float w0 = wave_max_g(m_max[0]), w1 = wave_max_g(m_max[1]);
+        if (g == 0) {
+          s_xm[wave][c] = w0;
+          s_xm[wave][16 + c] = w1;
+        }
+        barrier_lds();
+        m_ref[0] = fmaxf(w0, s_xm[partner][c]);
+        m_ref[1] = fmaxf(w1, s_xm[partner][16 + c]);
         comp = piece_cur;
         iss = piece_cur;
         j = piece_j;
         n_issued = piece_j;
         iss_valid = true;
         st1 = st2 = st3 = 0;
-        m_ref[0] = m_max[0];
-        m_ref[1] = m_max[1];
         attempt = 1;
         piece_start = true;
         prologue();
         continue;
       }
       attempt = 0;
+      const float l_tot[2] = {lw0 + s_xm[partner][c], lw1 + s_xm[partner][16 + c]};
 
-      // ---- finalise: lane holds heads 32hg+16hb+c, dims 256dh + 16db + 4g + (0..3)
-      const int b = rb + comp.b;
-      const int npieces = __builtin_amdgcn_readfirstlane(s_np[comp.b]);
+      // ---- finalise: lane holds heads 32hg+16hb+c, dims 256th + 16db + 4g + (0..3)
+      const int b = rb + comp.r;
+      const int npieces = __builtin_amdgcn_readfirstlane(s_np[comp.r]);
       int stores = 0;
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
         const int h = 32 * hg + 16 * hb + c;
-        const float l_tot = wave_sum_g(l_run[hb]);
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        const float lse_nat = l_tot > 0.f ? (m_ref[hb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+        const float inv = l_tot[hb] > 0.f ? 1.f / l_tot[hb] : 0.f;
+        const float lse_nat =
+            l_tot[hb] > 0.f ? (m_ref[hb] + log2f(l_tot[hb])) * 0.69314718055994531f : -INFINITY;
         if (npieces == 1) {
-          __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 256 * dh + 4 * g;
+          __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 256 * th + 4 * g;
 #pragma unroll
           for (int db = 0; db < 16; ++db) {
             u32x2 v;
@@ -363,18 +399,18 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
             *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
           }
           stores += 16;
-          if (p.lse != nullptr && dh == 0) {
+          if (p.lse != nullptr && th == 0) {
             if (g == 0) p.lse[(int64_t)b * p.lse_stride_b + h] = lse_nat;
             stores += 1;
           }
         } else {
-          const int slot = __builtin_amdgcn_readfirstlane(s_slot0[comp.b]) + w;
+          const int slot = __builtin_amdgcn_readfirstlane(s_slot0[comp.r]) + w;
           if (slot >= 0 && slot < p.ws_slots) {
-            float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * dh + 4 * g;
+            float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * th + 4 * g;
 #pragma unroll
             for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[hb][db] * inv;
             stores += 16;
-            if (dh == 0) {
+            if (th == 0) {
               if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
               stores += 1;
             }

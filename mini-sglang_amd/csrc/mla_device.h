@@ -73,21 +73,23 @@ __device__ __forceinline__ void sload_i32x4(const int32_t* ptr, int& a, int& b, 
   d = v[3];
 }
 
-// wait_vmcnt with a run-time (wave-uniform) count, clamped to the counter range.
-__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
-  n = n > 63 ? 63 : (n < 0 ? 0 : n);
-  switch (n) {
-#define MLA_VM_CASE(k) \
-  case k:              \
-    wait_vmcnt<k>();   \
-    break;
-#define MLA_VM_CASE8(k) MLA_VM_CASE(k) MLA_VM_CASE(k + 1) MLA_VM_CASE(k + 2) MLA_VM_CASE(k + 3) \
-    MLA_VM_CASE(k + 4) MLA_VM_CASE(k + 5) MLA_VM_CASE(k + 6) MLA_VM_CASE(k + 7)
-    MLA_VM_CASE8(0) MLA_VM_CASE8(8) MLA_VM_CASE8(16) MLA_VM_CASE8(24)
-    MLA_VM_CASE8(32) MLA_VM_CASE8(40) MLA_VM_CASE8(48) MLA_VM_CASE8(56)
-#undef MLA_VM_CASE8
-#undef MLA_VM_CASE
+// Binary tree of scalar branches over the wait count (6 compares for 0..63).
+template <int Lo, int Hi>
+__device__ __forceinline__ void wait_vmcnt_tree(int n) {
+  if constexpr (Lo == Hi) {
+    wait_vmcnt<Lo>();
+  } else {
+    constexpr int Mid = (Lo + Hi) / 2;
+    if (n <= Mid) wait_vmcnt_tree<Lo, Mid>(n);
+    else wait_vmcnt_tree<Mid + 1, Hi>(n);
   }
+}
+
+// wait_vmcnt with a run-time count, clamped to the counter range. The count is
+// made wave-uniform first so that the selection compiles to scalar branches.
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  n = __builtin_amdgcn_readfirstlane(n > 63 ? 63 : (n < 0 ? 0 : n));
+  wait_vmcnt_tree<0, 63>(n);
 }
 
 }  // namespace mla

@@ -53,6 +53,8 @@ PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
 MAX_PIECE_PAGES = 1024
+MAX_CTA_BLOCKS = 1024
+MAX_CTA_REQUESTS = 128
 
 
 class MLAKernelError(RuntimeError):

@@ -45,8 +45,11 @@ def test_plan_covers_every_token(ps, ctas):
     # a piece may touch at most MAX_PIECE_PAGES pages, and every further piece of a
     # request starts a new CTA, so the batch needs 1 + sum(pieces_b - 1) CTAs at least
     max_blk = (lib.MAX_PIECE_PAGES * ps if ps <= lib.PLAN_BLOCK else (lib.MAX_PIECE_PAGES - 1) * ps) // lib.PLAN_BLOCK
+    max_blk = min(max_blk, lib.MAX_CTA_BLOCKS)
     needed = 1 + sum(max(0, -(-(-(-L // lib.PLAN_BLOCK)) // max_blk) - 1) for L in lens)
-    if needed > ctas:
+    # and one CTA holds at most MAX_CTA_BLOCKS blocks
+    total_blocks = sum(-(-L // lib.PLAN_BLOCK) for L in lens)
+    if needed > ctas or -(-total_blocks // lib.MAX_CTA_BLOCKS) > ctas:
         with pytest.raises(lib.MLAKernelError):
             lib.decode_plan(lens, ps, ctas)
         return
