@@ -3,14 +3,17 @@
 Default workload (the headline one): Kimi-K2-shape absorbed-MLA paged decode,
 batch 64, 64 heads, 576-dim q / latent KV, page_size 64, random
 non-contiguous page table, seq_lens ~ U[1024, 8192], bf16 N(0,1) inputs.
-A "step" is one layer's decode attention over the batch: the split-KV
-kernel plus the LSE merge kernel, inputs resident in HBM. Two input sets
+A "step" is one layer's decode attention over the batch: one call of the
+library's decode entry point (split-KV kernel, then the LSE merge kernel),
+inputs resident in HBM. The same steps replayed from a HIP graph are reported
+as an extra field. Two input sets
 (680 MB of KV together, more than the 256 MB Infinity Cache) alternate so
 every step streams its KV from HBM.
 
 Prints one JSON line. ``value`` is the whole-step algorithmic HBM bandwidth
 (TB/s); µs/layer and tokens/s are extra fields. ``roofline`` times the
-dominant kernel (the split kernel) with HIP events on its launch stream.
+dominant kernel (the split kernel) alone, 16 back-to-back launches per HIP
+graph, with HIP events on its launch stream.
 ``cpu_baseline`` times the CPU oracle on a bounded sample of the same batch.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
@@ -28,7 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "mini-sglang_amd")]
 
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mla_decode_kimi_k2_b64_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mla_decode_kimi_k2_b64_traffic.md")
 
 
 def _decode_workload(device, seed):
@@ -80,13 +83,12 @@ def _cpu_baseline(case_gpu, budget_s: float = 12.0):
 def bench_decode(args):
     import torch
 
+    from minisgl_amd.benchmark.inputs import make_decode_case
     from minisgl_amd.kernel import lib
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     sets = [_decode_workload(dev, 0)]
-    from minisgl_amd.benchmark.inputs import make_decode_case
-
     # second input set: same lengths (so the same plan and work), different pages and values
     sets.append(make_decode_case(64, 64, 64, lens=sets[0].lens, device=dev, seed=100))
     case = sets[0]
@@ -100,41 +102,95 @@ def bench_decode(args):
     lse = torch.empty((B, H), dtype=torch.float32, device=dev)
     req_info = plan[ctas * lib.PLAN_CTA_INTS :]
     scale = (128 + 64) ** -0.5
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()  # default priority
 
-    def step(i, ev=None):
-        s = sets[i % 2]
-        if ev is not None:
-            ev[0].record(stream)
+    def split(s):
         lib.mla_decode(s.q, s.kv_pool, s.page_table, s.seq_lens, plan, ctas, ws_o, ws_lse, scale, out, lse,
                        stream=stream, split_only=True)
-        if ev is not None:
-            ev[1].record(stream)
-        lib.mla_decode_merge(ws_o, ws_lse, req_info, out, lse, stream=stream, single_piece_final=True)
-        if ev is not None:
-            ev[2].record(stream)
 
-    for i in range(args.warmup):
-        step(i)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i, events[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    split_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    merge_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
-    step_ms = wall * 1e3 / args.steps
-    dev_step_ms = events[0][0].elapsed_time(events[-1][2]) / args.steps
+    def merge():
+        lib.mla_decode_merge(ws_o, ws_lse, req_info, out, lse, stream=stream, single_piece_final=True)
+
+    def step(i):
+        split(sets[i % 2])
+        merge()
+
+    def layer(i):  # the one-call entry point: split kernel then merge kernel, launched from C++
+        c = sets[i % 2]
+        lib.mla_decode(c.q, c.kv_pool, c.page_table, c.seq_lens, plan, ctas, ws_o, ws_lse, scale, out, lse,
+                       stream=stream)
+
+    def capture(fn, n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(n):
+                fn(i)
+        return g
+
+    with torch.cuda.stream(stream):
+        # ---- timed: exactly args.steps layer steps, eager launches on one stream
+        for i in range(args.warmup):
+            layer(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(args.steps):
+            layer(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        step_ms = wall * 1e3 / args.steps
+        dev_step_ms = e0.elapsed_time(e1) / args.steps
+
+        # ---- the same steps replayed from one HIP graph (as a captured decode step), for reference;
+        # a replay must equal the eager result of the same launches
+        layer(0)
+        stream.synchronize()
+        ref_out = out.clone()
+        g_check = capture(layer, 1)
+        out.zero_()
+        g_check.replay()
+        stream.synchronize()
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16)), "graph replay differs from eager"
+        g_steps = capture(layer, args.steps)
+        g_steps.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        g_steps.replay()
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+
+        # ---- each kernel alone: back-to-back launches in one graph, HIP events on its stream
+        per_graph = 16
+        gs = capture(lambda i: split(sets[i % 2]), per_graph)
+        gm = capture(lambda i: merge(), per_graph)
+        gs.replay()
+        gm.replay()
+        torch.cuda.synchronize()
+        reps = 4
+
+        def timed(g):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                g.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / (reps * per_graph)
+
+        split_ms = timed(gs)
+        merge_ms = timed(gm)
 
     alg_bytes = case.algorithmic_bytes()
     value_tbps = alg_bytes / (step_ms * 1e-3) / 1e12
     achieved = alg_bytes / (split_ms * 1e-3) / 1e9
-    traffic = None
+    traffic = None  # HBM bytes per decode-kernel launch from the committed counter summary
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
     result = {
         "metric": "MLA decode achieved HBM TB/s + us/layer, Kimi-K2 shape, 1 MI355X",
         "value": round(value_tbps, 4),
@@ -163,6 +219,7 @@ def bench_decode(args):
         },
         "us_per_layer": round(step_ms * 1e3, 2),
         "us_per_layer_device": round(dev_step_ms * 1e3, 2),
+        "us_per_layer_graph": round(graph_ms * 1e3, 2),
         "tokens_per_s": round(B / (step_ms * 1e-3), 1),
         "split_kernel_us": round(split_ms * 1e3, 2),
         "merge_kernel_us": round(merge_ms * 1e3, 2),
@@ -174,7 +231,7 @@ def bench_decode(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "mla_decode_kernel<4,true> (split step)",
+            "kernel": "mla_decode_stream_kernel (split step)",
         },
     }
     if not args.no_cpu_baseline:

@@ -291,6 +291,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
 }
 
 // One wave per (request, head): lane holds dims 8*lane .. +8.
+// One wave per (request, head): lane i holds piece i's LSE (64 pieces per pass);
+// the partials are read 8 pieces at a time with all loads in flight together.
+constexpr int kMergeBatch = 8;
+
 __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
   const int b = blockIdx.x;
   const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
@@ -300,21 +304,18 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
   const int base = p.req_info[3 * b + 2];
   if (n == 1 && p.skip_single) return;
   __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 8 * lane;
+  auto piece_lse = [&](int i) {
+    const int s = base + i;
+    return (i < n && s >= 0 && s < p.ws_slots) ? p.ws_lse[(int64_t)s * p.heads + h] : -INFINITY;
+  };
 
   float mx = -INFINITY;
-  for (int i = lane; i < n; i += 64) {
-    const int s = base + i;
-    if (s >= 0 && s < p.ws_slots) mx = fmaxf(mx, p.ws_lse[(int64_t)s * p.heads + h]);
-  }
+  for (int i = lane; i < n; i += 64) mx = fmaxf(mx, piece_lse(i));
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   float sum = 0.f;
-  if (mx > -INFINITY) {
-    for (int i = lane; i < n; i += 64) {
-      const int s = base + i;
-      if (s >= 0 && s < p.ws_slots) sum += expf(p.ws_lse[(int64_t)s * p.heads + h] - mx);
-    }
-  }
+  if (mx > -INFINITY)
+    for (int i = lane; i < n; i += 64) sum += expf(piece_lse(i) - mx);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
   const bool any = mx > -INFINITY && sum > 0.f;
@@ -322,16 +323,31 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
 
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (any) {
-    for (int i = 0; i < n; ++i) {
-      const int s = base + i;
-      if (s < 0 || s >= p.ws_slots) continue;
-      const float wgt = expf(p.ws_lse[(int64_t)s * p.heads + h] - lse);
-      const f32x4* src = reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
-      const f32x4 a = src[0], bq = src[1];
+    for (int i0 = 0; i0 < n; i0 += 64) {
+      const float my_lse = piece_lse(i0 + lane);  // lane u: piece i0 + u
+      const int cnt = min(64, n - i0);
+      for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
+        f32x4 a[kMergeBatch], bq[kMergeBatch];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[j] += wgt * a[j];
-        acc[4 + j] += wgt * bq[j];
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const int s = base + i0 + u0 + u;
+          a[u] = bq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (u0 + u < cnt && s >= 0 && s < p.ws_slots) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
+            a[u] = src[0];
+            bq[u] = src[1];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const float l_u = __shfl(my_lse, u0 + u);
+          const float wgt = (u0 + u < cnt && l_u > -INFINITY) ? expf(l_u - lse) : 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[j] += wgt * a[u][j];
+            acc[4 + j] += wgt * bq[u][j];
+          }
+        }
       }
     }
   }
