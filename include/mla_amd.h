@@ -152,6 +152,34 @@ int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slot
                          int32_t single_piece_final, void *out, int64_t out_stride_b,
                          int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
 
+/*
+ * MLA chunked prefill (non-absorbed form), bf16 in, fp32 accumulate, bf16 out
+ * plus fp32 natural-log LSE. Causal and bottom-right aligned over a paged
+ * prefix: query i of request b (absolute position P_b + i, P_b = seq_lens_k[b]
+ * - extend_b) attends keys j <= P_b + i. Replaces the prefill attention call
+ * of BaseAttnBackend.forward (python/minisgl/attention/base.py:19-22; FA
+ * template python/minisgl/attention/fa.py:48-65 -> flash_attn_with_kvcache,
+ * fa.py:157-182) for MLA.
+ *   q         [total_q, heads, 192] strides (q_stride_t, q_stride_h); request b owns
+ *             rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1
+ *   k_pool    [num_pages, page_size, heads, 192], token row stride k_row_stride (>= heads*192)
+ *   v_pool    [num_pages, page_size, heads, 128], token row stride v_row_stride (>= heads*128)
+ *   page_table [batch, >= ceil(seq_lens_k[b]/page_size)] int32, row stride pt_stride
+ *   cu_seqlens_q [batch+1], seq_lens_k [batch] int32 device arrays; the K/V of all
+ *             seq_lens_k[b] tokens (prefix + extend) are already in the pools
+ *   out       [total_q, heads, 128] strides (out_stride_t, out_stride_h)
+ *   lse       [total_q, heads] fp32 (row stride lse_stride_t) or NULL
+ * page_size is a power of two >= 32; page ids outside [0, num_pages) are
+ * clamped into range.
+ */
+int mla_prefill_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, const void *k_pool,
+                     int64_t k_row_stride, const void *v_pool, int64_t v_row_stride,
+                     int32_t num_pages, int32_t page_size, const int32_t *page_table,
+                     int64_t pt_stride, const int32_t *cu_seqlens_q, const int32_t *seq_lens_k,
+                     int32_t batch, int32_t total_q, int32_t heads, float scale, void *out,
+                     int64_t out_stride_t, int64_t out_stride_h, float *lse, int64_t lse_stride_t,
+                     void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 2; }
+int mla_abi_version(void) { return 3; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -363,6 +363,63 @@ int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slot
   const mla::MergeParams m = merge_params(ws_o, ws_lse, ws_slots, req_info, batch, heads, single_piece_final ? 1 : 0,
                                           out, out_stride_b, out_stride_h, lse, lse_stride_b);
   return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_merge_f32 launch");
+}
+
+int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_pool, int64_t k_row_stride,
+                     const void* v_pool, int64_t v_row_stride, int32_t num_pages, int32_t page_size,
+                     const int32_t* page_table, int64_t pt_stride, const int32_t* cu_seqlens_q,
+                     const int32_t* seq_lens_k, int32_t batch, int32_t total_q, int32_t heads, float scale, void* out,
+                     int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t, void* stream) {
+  const char* who = "mla_prefill_bf16";
+  if (batch < 0 || total_q < 0 || heads < 1)
+    return fail(MLA_ERR_INVALID_ARG, "%s: batch %d, total_q %d, heads %d", who, batch, total_q, heads);
+  if (batch == 0 || total_q == 0) return ok();
+  if (q == nullptr || k_pool == nullptr || v_pool == nullptr || page_table == nullptr || cu_seqlens_q == nullptr ||
+      seq_lens_k == nullptr || out == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!is_pow2(page_size) || page_size < 32)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d must be a power of two >= 32", who, page_size);
+  if (num_pages < 1 || pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages / pt_stride < 1", who);
+  if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(out, 8))
+    return fail(MLA_ERR_INVALID_ARG, "%s: q/k/v must be 16-byte and out 8-byte aligned", who);
+  if (q_stride_t % 8 || q_stride_h % 8 || q_stride_h < mla::kPrefillQkDim)
+    return fail(MLA_ERR_INVALID_ARG, "%s: q strides (%lld, %lld) must be multiples of 8 with head stride >= 192", who,
+                (long long)q_stride_t, (long long)q_stride_h);
+  if (k_row_stride % 8 || k_row_stride < (int64_t)heads * mla::kPrefillQkDim || v_row_stride % 8 ||
+      v_row_stride < (int64_t)heads * mla::kPrefillVDim)
+    return fail(MLA_ERR_INVALID_ARG, "%s: k/v row strides (%lld, %lld) must be multiples of 8 and hold %d heads", who,
+                (long long)k_row_stride, (long long)v_row_stride, heads);
+  if ((int64_t)31 * k_row_stride * 2 + 384 > (int64_t)UINT32_MAX || (int64_t)31 * v_row_stride * 2 + 256 > (int64_t)UINT32_MAX)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: k/v row strides too large", who);
+  if (out_stride_t % 4 || out_stride_h % 4 || out_stride_h < mla::kPrefillVDim)
+    return fail(MLA_ERR_INVALID_ARG, "%s: out strides (%lld, %lld) must be multiples of 4 with head stride >= 128",
+                who, (long long)out_stride_t, (long long)out_stride_h);
+  if (lse != nullptr && lse_stride_t < heads)
+    return fail(MLA_ERR_INVALID_ARG, "%s: lse_stride_t %lld < heads", who, (long long)lse_stride_t);
+  if (!(scale > 0.f) || !isfinite(scale)) return fail(MLA_ERR_INVALID_ARG, "%s: bad scale", who);
+  mla::PrefillParams p;
+  p.q = static_cast<const __bf16*>(q);
+  p.q_stride_t = q_stride_t;
+  p.q_stride_h = q_stride_h;
+  p.k = static_cast<const __bf16*>(k_pool);
+  p.k_row_stride = k_row_stride;
+  p.v = static_cast<const __bf16*>(v_pool);
+  p.v_row_stride = v_row_stride;
+  p.num_pages = num_pages;
+  p.log2_ps = ilog2(page_size);
+  p.page_table = page_table;
+  p.pt_stride = pt_stride;
+  p.cu_seqlens_q = cu_seqlens_q;
+  p.seq_lens_k = seq_lens_k;
+  p.batch = batch;
+  p.heads = heads;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.out = static_cast<__bf16*>(out);
+  p.out_stride_t = out_stride_t;
+  p.out_stride_h = out_stride_h;
+  p.lse = lse;
+  p.lse_stride_t = lse_stride_t;
+  return hip_status(mla::launch_prefill(p, total_q, (hipStream_t)stream), "mla_prefill_bf16 launch");
 }
 
 }  // extern "C"

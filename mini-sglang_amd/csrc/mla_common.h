@@ -70,6 +70,33 @@ struct MergeParams {
   int64_t lse_stride_b;
 };
 
+// Chunked MLA prefill (non-absorbed): per-head K [.., 192] and V [.., 128] pools.
+constexpr int kPrefillQkDim = 192;
+constexpr int kPrefillVDim = 128;
+constexpr int kPrefillRows = 256;  // query rows per CTA (64 per wave)
+
+struct PrefillParams {
+  const __bf16* q;  // [T, H, 192]
+  int64_t q_stride_t, q_stride_h;
+  const __bf16* k;  // [pages * ps, H, 192]: token row stride k_row_stride, head stride 192
+  int64_t k_row_stride;
+  const __bf16* v;  // [pages * ps, H, 128]
+  int64_t v_row_stride;
+  int32_t num_pages;
+  int32_t log2_ps;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  const int32_t* cu_seqlens_q;  // [B + 1]
+  const int32_t* seq_lens_k;    // [B]: prefix + extend
+  int32_t batch, heads;
+  float scale_log2;
+  __bf16* out;  // [T, H, 128]
+  int64_t out_stride_t, out_stride_h;
+  float* lse;  // [T, H] or null
+  int64_t lse_stride_t;
+};
+
+hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_decode_stream(const DecodeParams& p, hipStream_t stream);  // heads 64, pages >= 32
 hipError_t launch_merge(const MergeParams& p, hipStream_t stream);

@@ -95,3 +95,75 @@ def make_decode_case(
         lens=lens,
         page_size=page_size,
     )
+
+
+QK_DIM = 192
+V_DIM = 128
+
+
+@dataclass
+class PrefillCase:
+    q: torch.Tensor  # bf16 [T, H, 192], requests packed by cu_seqlens_q
+    k_pool: torch.Tensor  # bf16 [num_pages, ps, H, 192]
+    v_pool: torch.Tensor  # bf16 [num_pages, ps, H, 128]
+    page_table: torch.Tensor  # int32 [B, max_pages]
+    cu_seqlens_q: torch.Tensor  # int32 [B + 1]
+    seq_lens_k: torch.Tensor  # int32 [B]: prefix + extend
+    extends: List[int]
+    prefixes: List[int]
+    page_size: int
+
+    def flops(self) -> int:
+        """Unmasked (query, key) pairs x H x 2 x (192 + 128)."""
+        H = self.q.shape[1]
+        pairs = sum(E * P + E * (E + 1) // 2 for E, P in zip(self.extends, self.prefixes))
+        return pairs * H * 2 * (QK_DIM + V_DIM)
+
+    def algorithmic_bytes(self) -> int:
+        """K/V of every key once, q, o, lse."""
+        T, H, _ = self.q.shape
+        keys = sum(E + P for E, P in zip(self.extends, self.prefixes))
+        return keys * H * (QK_DIM + V_DIM) * 2 + T * H * (QK_DIM + V_DIM) * 2 + T * H * 4
+
+
+def make_prefill_case(
+    heads: int,
+    page_size: int,
+    extends: Sequence[int],
+    prefixes: Sequence[int],
+    extra_pages: int = 1,
+    device: str | torch.device = "cpu",
+    seed: int = 0,
+) -> PrefillCase:
+    extends, prefixes = list(extends), list(prefixes)
+    lens = [E + P for E, P in zip(extends, prefixes)]
+    g_len = torch.Generator().manual_seed(seed)
+    num_pages = sum(-(-L // page_size) for L in lens) + extra_pages
+    pt = page_table_for(lens, page_size, num_pages, g_len)
+    dev = torch.device(device)
+    T = sum(extends)
+
+    def randn(shape, gen_seed):
+        if dev.type == "cpu":
+            return torch.randn(shape, generator=torch.Generator().manual_seed(gen_seed)).to(torch.bfloat16)
+        g = torch.Generator(device=dev).manual_seed(gen_seed)
+        out = torch.empty(shape, device=dev, dtype=torch.bfloat16)
+        flat = out.view(shape[0], -1)
+        step = max(1, (1 << 26) // flat.shape[1])
+        for r0 in range(0, shape[0], step):
+            r1 = min(shape[0], r0 + step)
+            flat[r0:r1] = torch.randn((r1 - r0, flat.shape[1]), generator=g, device=dev).to(torch.bfloat16)
+        return out
+
+    q = randn((T, heads, QK_DIM), seed + 1)
+    k = randn((num_pages, page_size, heads, QK_DIM), seed + 2)
+    v = randn((num_pages, page_size, heads, V_DIM), seed + 3)
+    cu = [0]
+    for E in extends:
+        cu.append(cu[-1] + E)
+    return PrefillCase(
+        q=q, k_pool=k, v_pool=v, page_table=pt.to(dev),
+        cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=dev),
+        seq_lens_k=torch.tensor(lens, dtype=torch.int32, device=dev),
+        extends=extends, prefixes=prefixes, page_size=page_size,
+    )

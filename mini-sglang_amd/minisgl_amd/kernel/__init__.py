@@ -7,6 +7,7 @@ from .lib import (
     load_library,
     mla_decode,
     mla_decode_merge,
+    mla_prefill,
     page_table_from_tokens,
     store_rows,
 )
@@ -18,6 +19,7 @@ __all__ = [
     "load_library",
     "mla_decode",
     "mla_decode_merge",
+    "mla_prefill",
     "page_table_from_tokens",
     "store_rows",
 ]

@@ -46,9 +46,14 @@ SIGNATURES = {
     "mla_decode_merge_f32": (
         ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _vp]
     ),
+    "mla_prefill_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, ctypes.c_float,
+         _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -212,4 +217,34 @@ def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None, single_
             _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
         ),
         "mla_decode_merge_f32",
+    )
+
+
+def mla_prefill(q, k_pool, v_pool, page_table, cu_seqlens_q, seq_lens_k, scale: float, out, lse=None,
+                stream=None) -> None:
+    """Chunked MLA prefill: ``q [T, H, 192]``, ``k_pool [pages, ps, H, 192]``, ``v_pool [pages, ps, H, 128]``
+    -> ``out [T, H, 128]`` (+ ``lse [T, H]``); causal over each request's prefix + extend."""
+    import torch
+
+    T, H, D = q.shape
+    assert D == 192 and q.dtype == torch.bfloat16 and q.stride(-1) == 1
+    assert k_pool.dim() == 4 and k_pool.shape[2:] == (H, 192) and v_pool.shape[2:] == (H, 128)
+    assert k_pool.dtype == torch.bfloat16 and v_pool.dtype == torch.bfloat16
+    assert k_pool.stride(3) == 1 and k_pool.stride(2) == 192 and v_pool.stride(3) == 1 and v_pool.stride(2) == 128
+    assert k_pool.stride(0) == k_pool.shape[1] * k_pool.stride(1) and v_pool.stride(0) == v_pool.shape[1] * v_pool.stride(1)
+    assert k_pool.shape[:2] == v_pool.shape[:2]
+    assert page_table.dtype == torch.int32 and cu_seqlens_q.dtype == torch.int32 and seq_lens_k.dtype == torch.int32
+    assert out.shape == (T, H, 128) and out.dtype == torch.bfloat16 and out.stride(-1) == 1
+    B = seq_lens_k.shape[0]
+    assert cu_seqlens_q.shape[0] == B + 1
+    if lse is not None:
+        assert lse.dtype == torch.float32 and lse.shape == (T, H) and lse.stride(-1) == 1
+    check(
+        load_library().mla_prefill_bf16(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(k_pool), k_pool.stride(1), _ptr(v_pool), v_pool.stride(1),
+            k_pool.shape[0], k_pool.shape[1], _ptr(page_table), page_table.stride(0), _ptr(cu_seqlens_q),
+            _ptr(seq_lens_k), B, T, H, float(scale), _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+            0 if lse is None else lse.stride(0), _stream(stream),
+        ),
+        "mla_prefill_bf16",
     )
