@@ -239,19 +239,80 @@ def bench_decode(args):
     return result
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(args):
+    """Chunked MLA prefill, B=4, H=64, extend 2048 each, prefixes U[0, 8192], page 64 (one layer)."""
+    import torch
+
+    from minisgl_amd.benchmark.inputs import make_prefill_case
+    from minisgl_amd.kernel import lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(0)
+    prefixes = torch.randint(0, 8193, (4,), generator=g).tolist()
+    case = make_prefill_case(64, 64, extends=[2048] * 4, prefixes=prefixes, device=dev, seed=0)
+    T, H, _ = case.q.shape
+    out = torch.empty((T, H, 128), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()
+    scale = (128 + 64) ** -0.5
+
+    def layer():
+        lib.mla_prefill(case.q, case.k_pool, case.v_pool, case.page_table, case.cu_seqlens_q, case.seq_lens_k,
+                        scale, out, lse, stream=stream)
+
+    steps = max(1, args.steps // 5)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup // 5)):
+            layer()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            layer()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    step_ms = wall * 1e3 / steps
+    kern_ms = e0.elapsed_time(e1) / steps
+    flops = case.flops()
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    return {
+        "workload": "MLA chunked prefill, one layer: B=4, H=64, extend 2048, prefix U[0,8192], qk 192, v 128, page 64",
+        "prefixes": prefixes,
+        "us_per_layer": round(step_ms * 1e3, 1),
+        "kernel_us": round(kern_ms * 1e3, 1),
+        "tokens_per_s": round(T / (step_ms * 1e-3), 1),
+        "tflops": round(achieved, 1),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "algorithmic_flops": flops,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill"])
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill summary of the decode line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part "
               "of this build", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "prefill":
+        print(json.dumps(bench_prefill(args)))
+        return
     res = bench_decode(args)
+    if not args.no_prefill:
+        res["prefill"] = bench_prefill(args)
     print(json.dumps(res))
 
 

@@ -169,8 +169,8 @@ int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slot
  *             seq_lens_k[b] tokens (prefix + extend) are already in the pools
  *   out       [total_q, heads, 128] strides (out_stride_t, out_stride_h)
  *   lse       [total_q, heads] fp32 (row stride lse_stride_t) or NULL
- * page_size is a power of two >= 32; page ids outside [0, num_pages) are
- * clamped into range.
+ * page_size is a power of two >= 64 (one 64-token key tile lies in one page);
+ * page ids outside [0, num_pages) are clamped into range.
  */
 int mla_prefill_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, const void *k_pool,
                      int64_t k_row_stride, const void *v_pool, int64_t v_row_stride,

@@ -377,8 +377,8 @@ int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   if (q == nullptr || k_pool == nullptr || v_pool == nullptr || page_table == nullptr || cu_seqlens_q == nullptr ||
       seq_lens_k == nullptr || out == nullptr)
     return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
-  if (!is_pow2(page_size) || page_size < 32)
-    return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d must be a power of two >= 32", who, page_size);
+  if (!is_pow2(page_size) || page_size < 64)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d must be a power of two >= 64", who, page_size);
   if (num_pages < 1 || pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages / pt_stride < 1", who);
   if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(out, 8))
     return fail(MLA_ERR_INVALID_ARG, "%s: q/k/v must be 16-byte and out 8-byte aligned", who);

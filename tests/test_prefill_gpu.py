@@ -40,7 +40,7 @@ def check_case(case):
     torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
 
 
-@pytest.mark.parametrize("ps", [32, 64, 128])
+@pytest.mark.parametrize("ps", [64, 128, 256])
 def test_prefill_ragged(ps):
     """Extends that are not multiples of 256 (or 32), prefixes that split pages."""
     case = make_prefill_case(8, ps, extends=[1, 37, 256, 300], prefixes=[0, 95, 64, 513], seed=ps)
@@ -74,6 +74,12 @@ def test_prefill_single_token_extend_is_decode_like():
 def test_prefill_long_extend_multiple_blocks():
     case = make_prefill_case(4, 64, extends=[1024, 700], prefixes=[1500, 3], seed=12)
     check_case(case)
+
+
+def test_prefill_small_pages_rejected():
+    case = make_prefill_case(2, 32, extends=[10], prefixes=[5], seed=1)
+    with pytest.raises(lib.MLAKernelError, match="page_size"):
+        run_prefill(case)
 
 
 def test_prefill_growing_logits_rescale():
