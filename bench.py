@@ -294,25 +294,157 @@ def bench_prefill(args):
     }
 
 
+class _DecodeCall:
+    """Plan, workspace and outputs of one decode batch; ``__call__`` is one layer's one-call decode."""
+
+    def __init__(self, case, dev):
+        import torch
+
+        from minisgl_amd.kernel import lib
+
+        self.lib, self.case = lib, case
+        B, H, _ = case.q.shape
+        self.ctas = lib.device_cu_count(0)
+        plan_np, self.slots = lib.decode_plan(case.lens, case.page_size, self.ctas)
+        self.plan = torch.from_numpy(plan_np).to(dev)
+        self.ws_o = torch.empty((max(self.slots, 1), H, 512), dtype=torch.float32, device=dev)
+        self.ws_lse = torch.empty((max(self.slots, 1), H), dtype=torch.float32, device=dev)
+        self.out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty((B, H), dtype=torch.float32, device=dev)
+
+    def __call__(self, stream):
+        c = self.case
+        self.lib.mla_decode(c.q, c.kv_pool, c.page_table, c.seq_lens, self.plan, self.ctas, self.ws_o, self.ws_lse,
+                            (128 + 64) ** -0.5, self.out, self.lse, stream=stream)
+
+
+class _PrefillCall:
+    def __init__(self, case, dev):
+        import torch
+
+        from minisgl_amd.kernel import lib
+
+        self.lib, self.case = lib, case
+        T, H, _ = case.q.shape
+        self.out = torch.empty((T, H, 128), dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+
+    def __call__(self, stream):
+        c = self.case
+        self.lib.mla_prefill(c.q, c.k_pool, c.v_pool, c.page_table, c.cu_seqlens_q, c.seq_lens_k, (128 + 64) ** -0.5,
+                             self.out, self.lse, stream=stream)
+
+
+def _time_device(fn, stream, steps, warmup):
+    """Mean device time (ms) of ``fn()`` over ``steps`` launches on ``stream`` (HIP events on that stream)."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def bench_long_context(args):
+    """Long-context split-KV decode: B=8, H=64, lengths U[32768, 131072], page 64 (one layer)."""
+    import torch
+
+    from minisgl_amd.benchmark.inputs import make_decode_case
+
+    dev = torch.device("cuda:0")
+    case = make_decode_case(8, 64, 64, len_range=(32768, 131072), device=dev, seed=0)
+    call = _DecodeCall(case, dev)
+    stream = torch.cuda.Stream()
+    ms = _time_device(lambda: call(stream), stream, max(2, args.steps // 5), max(1, args.warmup // 5))
+    alg = case.algorithmic_bytes()
+    res = {
+        "workload": "long-context absorbed-MLA decode, one layer: B=8, H=64, seq U[32768,131072], page 64",
+        "kv_tokens": sum(case.lens),
+        "partial_slots": call.slots,
+        "us_per_layer": round(ms * 1e3, 1),
+        "tb_per_s": round(alg / (ms * 1e-3) / 1e12, 3),
+        "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+    del case, call
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_mixed(args):
+    """Ragged batch sharing radix prefixes: 32 decode requests (ctx U[512,16384]) + 4 prefill chunks of
+    1024 tokens on 2048-token shared prefixes (8 groups), 64 heads, page 64 (one layer).
+
+    Reported three ways: each half alone, both on one stream, and the two halves on two streams
+    (HBM-bound decode beside MFMA-bound prefill)."""
+    import torch
+
+    from minisgl_amd.benchmark.inputs import make_mixed_case
+
+    dev = torch.device("cuda:0")
+    m = make_mixed_case(32, 4, 64, 64, (512, 16384), 1024, 2048, 8, device=dev, seed=0)
+    dec, pre = _DecodeCall(m.decode, dev), _PrefillCall(m.prefill, dev)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    steps, warm = max(2, args.steps // 5), max(1, args.warmup // 5)
+    dec_ms = _time_device(lambda: dec(s1), s1, steps, warm)
+    pre_ms = _time_device(lambda: pre(s1), s1, steps, warm)
+    seq_ms = _time_device(lambda: (dec(s1), pre(s1)), s1, steps, warm)
+
+    def both():  # fork s2 off s1, join back
+        ev = torch.cuda.Event()
+        ev.record(s1)
+        s2.wait_event(ev)
+        pre(s2)
+        dec(s1)
+        ev2 = torch.cuda.Event()
+        ev2.record(s2)
+        s1.wait_event(ev2)
+
+    par_ms = _time_device(both, s1, steps, warm)
+    res = {
+        "workload": "mixed ragged batch, one layer: 32 decode (ctx U[512,16384]) + 4 prefill chunks of 1024 on "
+        "2048-token shared prefixes (8 groups), H=64, page 64",
+        "decode_us": round(dec_ms * 1e3, 1),
+        "prefill_us": round(pre_ms * 1e3, 1),
+        "one_stream_us_per_layer": round(seq_ms * 1e3, 1),
+        "two_streams_us_per_layer": round(par_ms * 1e3, 1),
+        "tokens_per_layer": len(m.decode.lens) + sum(m.prefill.extends),
+    }
+    del m, dec, pre
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed"])
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill summary of the decode line")
+    ap.add_argument("--no-extra", action="store_true", help="skip the long-context and mixed-batch summaries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part "
               "of this build", file=sys.stderr)
         sys.exit(2)
-    if args.workload == "prefill":
-        print(json.dumps(bench_prefill(args)))
+    one = {"prefill": bench_prefill, "long": bench_long_context, "mixed": bench_mixed}
+    if args.workload in one:
+        print(json.dumps(one[args.workload](args)))
         return
     res = bench_decode(args)
     if not args.no_prefill:
         res["prefill"] = bench_prefill(args)
+    if not args.no_extra:
+        res["long_context"] = bench_long_context(args)
+        res["mixed"] = bench_mixed(args)
     print(json.dumps(res))
 
 

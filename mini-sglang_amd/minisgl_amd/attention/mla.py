@@ -10,9 +10,11 @@ with the attention math in libmla_amd.so:
   gather kernel) and -- for decode -- a split-KV plan computed on the host by
   the library's planner (the role FlashInfer's plan() plays in fi.py:123-166).
   Host arrays go to the device with pinned non-blocking copies (fa.py:76-90).
-* ``forward`` stores the new latent rows into the pool (fa.py:53) and runs the
-  absorbed decode kernel: ``q [B, H, 576]`` -> ``o [B, H, 512]`` (latent
-  space; the caller applies W_UV).
+* ``forward`` stores the new rows into the pool (fa.py:53) and runs, for a
+  decode batch, the absorbed decode kernel: ``q [B, H, 576]`` -> ``o [B, H,
+  512]`` (latent space; the caller applies W_UV); for a prefill batch, the
+  chunked prefill kernel over the per-head K/V pages: ``q [T, H, 192]`` -> ``o
+  [T, H, 128]``.
 * the capture hooks point the metadata at static buffers sized for the
   largest captured batch (fa.py:107-136); replay copies the live metadata in.
 """
@@ -92,13 +94,28 @@ class MLAAttnBackend(BaseAttnBackend):
         assert isinstance(metadata, MLAMetadata)
         self.kvcache.store_kv(k, v, batch.out_loc, layer_id)
         if not metadata.is_decode:
-            raise NotImplementedError("MLA chunked prefill is not available in this build of libmla_amd")
+            return self._forward_prefill(q, layer_id, metadata)
         B, H, _ = q.shape
         out = torch.empty((B, H, self.config.kv_lora_rank), dtype=q.dtype, device=q.device)
         lse = torch.empty((B, H), dtype=torch.float32, device=q.device)
         lib.mla_decode(
             q, self.kvcache.latent_cache(layer_id), metadata.page_table, metadata.cache_seqlens, metadata.plan,
             self.num_ctas, self.ws_o, self.ws_lse, self.scale, out, lse,
+        )
+        self.last_lse = lse
+        return out
+
+    def _forward_prefill(self, q: torch.Tensor, layer_id: int, metadata: MLAMetadata) -> torch.Tensor:
+        """Chunked prefill, non-absorbed: ``q [T, H, 192]`` over the per-head K/V pages -> ``[T, H, 128]``.
+
+        The new tokens' K/V were stored above; every request attends its prefix and itself causally
+        (bottom-right aligned, ``attention/fa.py:155``)."""
+        T, H, _ = q.shape
+        out = torch.empty((T, H, self.config.v_head_dim), dtype=q.dtype, device=q.device)
+        lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
+        lib.mla_prefill(
+            q, self.kvcache.prefill_k_cache(layer_id), self.kvcache.prefill_v_cache(layer_id), metadata.page_table,
+            metadata.cu_seqlens_q, metadata.cache_seqlens, self.scale, out, lse,
         )
         self.last_lse = lse
         return out

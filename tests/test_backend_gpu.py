@@ -121,3 +121,60 @@ def test_backend_decode_graph_replay():
         _ = (q.float() * 2).sum().item()
         for r in reqs:
             r.complete_one()
+
+
+def test_backend_prefill_with_prefix():
+    """A prefill batch through the backend: the new per-head K/V rows are stored
+    at out_loc, then every request attends its cached prefix and itself causally."""
+    reset_global_ctx()
+    page_size, H = 64, 16
+    ctx = Context(page_size=page_size)
+    set_global_ctx(ctx)
+    gen = torch.Generator().manual_seed(5)
+    cfg = MLAConfig(num_heads=H, num_layers=2)
+    cached, extends = [0, 130, 64, 700], [300, 1, 77, 129]
+    lens = [c + e for c, e in zip(cached, extends)]
+    need = [-(-L // page_size) for L in lens]
+    num_pages = sum(need) + 3
+    pool = create_kvcache_pool(cfg, num_pages, page_size, torch.bfloat16, DEV, with_prefill_pages=True)
+    ctx.kv_cache = pool
+    tt = torch.zeros((len(lens) + 1, 1024), dtype=torch.int32)
+    starts = torch.randperm(num_pages, generator=gen)[: sum(need)] * page_size
+    off = 0
+    for r, n in enumerate(need):
+        tt[r, : n * page_size] = (starts[off : off + n].unsqueeze(1) + torch.arange(page_size)).flatten().to(torch.int32)
+        off += n
+    ctx.page_table = tt.to(DEV)
+    layer = 1
+    kc, vc = pool.prefill_k_cache(layer), pool.prefill_v_cache(layer)
+    kc.copy_(torch.randn(kc.shape, generator=gen).to(torch.bfloat16).to(DEV))
+    vc.copy_(torch.randn(vc.shape, generator=gen).to(torch.bfloat16).to(DEV))
+    backend = create_attention_backend("mla", cfg)
+    ctx.attn_backend = backend
+
+    reqs = [Req(table_idx=i, cached_len=c, device_len=c + e) for i, (c, e) in enumerate(zip(cached, extends))]
+    batch = Batch(reqs=reqs, phase="prefill")
+    batch.padded_reqs = reqs
+    locs = [int(tt[r.table_idx, t]) for r in reqs for t in range(r.cached_len, r.device_len)]
+    batch.out_loc = torch.tensor(locs, dtype=torch.int32, device=DEV)
+    backend.prepare_metadata(batch)
+    T = sum(extends)
+    q = torch.randn((T, H, 192), generator=gen).to(torch.bfloat16).to(DEV)
+    k_new = torch.randn((T, H, 192), generator=gen).to(torch.bfloat16).to(DEV)
+    v_new = torch.randn((T, H, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    with ctx.forward_batch(batch):
+        o = backend.forward(q, k_new, v_new, layer, batch)
+    torch.cuda.synchronize()
+    loc = batch.out_loc.long()
+    assert torch.equal(kc.reshape(-1, H, 192)[loc].view(torch.int16), k_new.view(torch.int16))
+    assert torch.equal(vc.reshape(-1, H, 128)[loc].view(torch.int16), v_new.view(torch.int16))
+
+    idx = torch.arange(len(reqs), dtype=torch.int32)
+    pt = R.page_table_from_tokens(tt, idx, max(lens), page_size)
+    cu = torch.tensor([0] + extends, dtype=torch.int32).cumsum(0).to(torch.int32)
+    o_ref, lse_ref = R.mla_prefill(q.cpu(), kc.cpu(), vc.cpu(), pt, cu, torch.tensor(lens, dtype=torch.int32))
+    assert o.shape == (T, H, 128)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
+    md = batch.attn_metadata
+    assert torch.equal(md.get_last_indices(len(reqs)).cpu(), cu[1:] - 1)

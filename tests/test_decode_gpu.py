@@ -184,3 +184,14 @@ def test_split_then_merge_equals_one_call():
         outs.append((out.cpu(), lse.cpu()))
     assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
     assert torch.equal(outs[0][1], outs[1][1])
+
+
+def test_decode_long_context_split_kv():
+    """Batch 8, 64 heads, lengths U[32768, 131072] (page_size 64): every request
+    is split over many CTAs and merged through the fp32 LSE."""
+    case = make_decode_case(8, 64, 64, len_range=(32768, 131072), device=DEV, seed=0)
+    out, lse, slots = run_decode(case.q, case.kv_pool, case.page_table, case.seq_lens, case.lens, 64, 256)
+    assert slots > 8  # split-KV really happened
+    o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
+    torch.testing.assert_close(out, o_ref, **O_TOL)
+    torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
