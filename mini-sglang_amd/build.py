@@ -31,9 +31,14 @@ FLAGS = [
 ]
 
 
+# per-source device flags: the prefill kernel's softmax needs no NaN handling in fmax (its scores
+# are finite or -inf), which saves a canonicalising instruction per operand
+SOURCE_FLAGS = {"mla_prefill.hip": ["-Xarch_device", "-fno-honor-nans"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)

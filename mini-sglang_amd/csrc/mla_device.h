@@ -43,10 +43,10 @@ __device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base)
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  // round-to-nearest-even, matching torch's float->bfloat16 conversion
-  __bf16 x = (__bf16)a, y = (__bf16)b;
-  uint16_t ux = __builtin_bit_cast(uint16_t, x), uy = __builtin_bit_cast(uint16_t, y);
-  return (uint32_t)ux | ((uint32_t)uy << 16);
+  // round-to-nearest-even, matching torch's float->bfloat16 conversion; one v_cvt_pk_bf16_f32
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 

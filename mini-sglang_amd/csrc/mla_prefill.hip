@@ -2,25 +2,29 @@
 // a paged prefix: query i of a request with prefix P attends keys j <= P + i.
 // Per head: q [192] (128 nope + 64 rope), K [192], V [128].
 //
-// One CTA per (request, 256 query rows, head); 4 waves x 64 query rows.
-//  * K/V tiles of 64 tokens (K 24 KB + V 16 KB) are staged by 16-byte DMA
-//    loads into a 3-stage LDS ring. K rows (384 B) are stored with the 16-byte
-//    chunk index XOR (token & 7) inside each 8-chunk group, V rows (256 B) with
-//    XOR 2 * (token & 3): both the K operand reads and the transposing V reads
-//    are then bank-conflict free.
-//  * S^T[32 keys x 32 queries] = K . Q^T on 32x32x16 bf16 MFMA, two key halves
-//    x two 32-row query sub-blocks per tile; each K read feeds both
-//    sub-blocks. The wave's queries live in accumulation registers as the B
-//    operand. Each lane holds 16 keys of one query per key half: the row max
-//    needs one cross-half shuffle and the softmax numerators P^T are already
-//    in the B-operand layout of O^T[128 dims x 32 queries] += V^T . P^T (k
-//    order permuted consistently in the V^T reads); each V^T read feeds both
-//    sub-blocks.
+// One CTA per (request, 256 query rows, head); 4 waves x 64 query rows (two
+// 32-row sub-blocks), one wave per SIMD.
+//  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 7-stage
+//    LDS ring filled by 16-byte DMA loads. K rows (384 B) are stored with the
+//    16-byte chunk index XOR (token & 7) inside each 8-chunk group, V rows
+//    (256 B) with XOR 2 * (token & 3): the K operand reads and the transposing
+//    V reads are then bank-conflict free.
+//  * S^T[32 keys x 32 queries] = K . Q^T and O^T[128 dims x 32 queries] +=
+//    V^T . P^T on 32x32x16 bf16 MFMA; the queries stay in accumulation
+//    registers as the B operand, O in accumulation registers; each K and V^T
+//    read feeds both sub-blocks.
+//  * Software pipeline over the stages: step j issues the value MFMAs of stage
+//    j-1 and the score MFMAs of stage j+1 while the vector ALU runs the online
+//    softmax of stage j, the two instruction streams interleaved slot by slot
+//    (one MFMA per slot). Steps that need masking (the diagonal), and the
+//    first and last steps of a wave, run the three parts one after another.
 //  * Online softmax in the log2 domain with lazy rescaling: the running max
-//    moves (and O, l are rescaled) only when a tile's max exceeds it by 8.
+//    moves (and O, l are rescaled) only when a stage's max exceeds it by 8.
 //  * The heads of one (request, query block) are consecutive CTAs, so the
 //    query blocks of one head are 'heads' CTAs apart and, with heads a
 //    multiple of 8, land on the same XCD and share its L2 for K/V.
+#include <type_traits>
+
 #include "mla_common.h"
 #include "mla_device.h"
 
@@ -31,18 +35,39 @@ typedef float f32x16_t __attribute__((__vector_size__(64)));
 
 constexpr int kPWaves = 4;
 constexpr int kPRowsPerWave = kPrefillRows / kPWaves;  // 64
-constexpr int kPTile = 64;                              // keys per tile (one page: page_size >= 64)
+constexpr int kPStage = 32;                             // keys per stage
 constexpr int kPKRowBytes = kPrefillQkDim * 2;          // 384
 constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
-constexpr int kPKBytes = kPTile * kPKRowBytes;          // 24576
-constexpr int kPVBytes = kPTile * kPVRowBytes;          // 16384
-constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 40960
-constexpr int kPStages = 3;
-constexpr int kPKDma = kPKBytes / 1024 / kPWaves;  // 6 wave-wide DMA loads per wave
-constexpr int kPVDma = kPVBytes / 1024 / kPWaves;  // 4
-constexpr int kPDma = kPKDma + kPVDma;             // 10
+constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
+constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
+constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
+constexpr int kPStages = 7;
+constexpr int kPKDma = kPKBytes / 1024 / kPWaves;  // 3 wave-wide DMA loads per wave
+constexpr int kPVDma = kPVBytes / 1024 / kPWaves;  // 2
+constexpr int kPDma = kPKDma + kPVDma;             // 5
 constexpr float kPRescaleLog2 = 8.0f;
-constexpr int kPMaxPages = 4096;  // page ids of a CTA's keys staged in LDS (else read per tile)
+constexpr int kPMaxPages = 1024;  // page ids of a CTA's keys staged in LDS (else read per stage)
+
+// ---- the softmax of one stage as a list of micro-operations, spread over the 40 MFMA slots of a
+// pipelined step in proportion to their cost (4-cycle units; exp2 is a quarter-rate instruction):
+//   u in [0, 16): running max over two scores (sub-block u / 8)
+//   u in [16, 18): max across the two wave halves
+//   u in [18, 20): reference update, rescale factor, -m
+//   u in [20, 68): v = u - 20, k = v / 6, r = v % 6, sub-block r / 3: r % 3 < 2 -> exp2 of score
+//                  2k + r % 3 and its sum; r % 3 == 2 -> pack scores 2k, 2k + 1 to bf16
+constexpr int kSlots = 40;  // 16 value MFMAs + 24 score MFMAs
+constexpr int kUops = 68;
+constexpr int uop_weight(int u) { return u < 16 ? 1 : u < 18 ? 2 : u < 20 ? 10 : ((u - 20) % 3 == 2 ? 1 : 6); }
+constexpr int uop_total() {
+  int t = 0;
+  for (int u = 0; u < kUops; ++u) t += uop_weight(u);
+  return t;
+}
+constexpr int uop_slot(int u) {
+  int t = 0;
+  for (int v = 0; v < u; ++v) t += uop_weight(v);
+  return t * kSlots / uop_total();
+}
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -51,25 +76,55 @@ __device__ __forceinline__ int wave_sum(int v) {
 }
 __device__ __forceinline__ int kswz(int c, int t) { return (c & ~7) | ((c & 7) ^ (t & 7)); }
 __device__ __forceinline__ int vswz(int c, int t) { return c ^ (2 * (t & 3)); }
+// max / sum of a lane's value with lane ^ 32 (v_permlane32_swap, no LDS traffic)
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
-// S^T += K . Q^T with the query operand read straight from accumulation registers (where the queries
-// live for the whole kernel), so the compiler does not copy them per MFMA. A chain accumulates in
-// place; its first k-step starts from zero.
+// S^T += K . Q^T with the query operand read straight from accumulation registers. A chain
+// accumulates in place; its first k-step starts from zero.
 __device__ __forceinline__ void mfma_qk_first(f32x16_t& d, const bf16x8& k, const bf16x8& q) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "a"(q));
 }
 __device__ __forceinline__ void mfma_qk(f32x16_t& d, const bf16x8& k, const bf16x8& q) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "a"(q));
 }
-// The scores written by the chains above are read by vector ALU instructions next: wait states
-// between the last MFMA's write and the first read (24 >= what a 16-pass MFMA needs).
-__device__ __forceinline__ void mfma_result_wait(f32x16_t& a, f32x16_t& b, f32x16_t& c, f32x16_t& d) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+// O^T += V^T . P^T (the compiler places O and tracks its hazards).
+__device__ __forceinline__ void mfma_pv(f32x16_t& o, const bf16x8& v, const u32x4& p) {
+  o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, __builtin_bit_cast(bf16x8, p), o, 0, 0, 0);
+}
+// The score MFMAs are opaque to the compiler's hazard tracking: before the vector ALU reads their
+// results, wait out the pipeline (24 wait states >= what a 16-pass MFMA needs).
+__device__ __forceinline__ void mfma_wait_scores(f32x16_t& a, f32x16_t& b) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
+
+// Pin a vector-ALU result to its place in the instruction stream: the empty volatile asm is
+// ordered with the MFMA asm statements, so the computation cannot drift into another slot.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+// f(ic<0>{}), ..., f(ic<N-1>{}): a loop whose index is a compile-time constant in the body
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(ic<I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kPStages * kPStageBytes];
   __shared__ int s_pg[kPMaxPages];
+  __shared__ __attribute__((aligned(1024))) char s_dummy[1024];  // destination of dummy DMA groups
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -77,7 +132,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 
   // ---- work item: request b, query block qb, head h (heads fastest); the last items (the
   // latest query blocks, which see the most keys) are dispatched first
-  auto items_of = [&](int r) {
+  auto items_of = [&](int r) __attribute__((always_inline)) {
     return r < p.batch ? ((p.cu_seqlens_q[r + 1] - p.cu_seqlens_q[r] + kPrefillRows - 1) / kPrefillRows) * H : 0;
   };
   int total = 0;
@@ -118,30 +173,31 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   const int row0 = qb * kPrefillRows + wave * kPRowsPerWave;  // this wave's first query row in the request
   const int cta_rows_end = min(E, (qb + 1) * kPrefillRows);
   const int nkeys = P + cta_rows_end;  // keys the CTA needs
-  const int ntiles = (nkeys + kPTile - 1) / kPTile;
+  const int nst = __builtin_amdgcn_readfirstlane((nkeys + kPStage - 1) / kPStage);
   const int wave_rows = max(0, min(E - row0, kPRowsPerWave));
-  const int wave_tiles = wave_rows > 0 ? (P + row0 + wave_rows + kPTile - 1) / kPTile : 0;
+  const int W =  // stages this wave needs
+      __builtin_amdgcn_readfirstlane(wave_rows > 0 ? (P + row0 + wave_rows + kPStage - 1) / kPStage : 0);
 
   const int g32 = lane >> 5;  // half of the wave
   const int c32 = lane & 31;
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
+  const uint32_t lds_dummy = (uint32_t)(uintptr_t)(MLA_LDS char*)s_dummy;
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * kPKRowBytes;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * kPVRowBytes;
   const int krow_bytes = (int)(p.k_row_stride * 2), vrow_bytes = (int)(p.v_row_stride * 2);
 
   // ---- page ids of the CTA's keys
-  const int npages = (nkeys + ps_mask) >> p.log2_ps;
+  const int npages = __builtin_amdgcn_readfirstlane((nkeys + ps_mask) >> p.log2_ps);
   const bool staged = npages <= kPMaxPages;
-  if (staged) {
-    for (int i = threadIdx.x; i < npages; i += 256)
-      s_pg[i] = min(max(p.page_table[(int64_t)b * p.pt_stride + i], 0), p.num_pages - 1);
-    __syncthreads();
-  }
+  // (unstaged, s_pg[0] still holds the first page: the source of dummy DMA groups)
+  for (int i = threadIdx.x; i < (staged ? npages : 1); i += 256)
+    s_pg[i] = min(max(p.page_table[(int64_t)b * p.pt_stride + i], 0), p.num_pages - 1);
+  __syncthreads();
 
-  // ---- DMA of key tile n (64 tokens of one page); rows past the last key load the last key.
-  // LDS position s (16 bytes each) of the K tile holds token s / 24, chunk kswz(s % 24); of the V tile
-  // token s / 16, chunk vswz(s % 16).
+  // ---- DMA of stage n (32 tokens of one page: page_size >= 64); rows past the last key load the
+  // last key. LDS position s (16 bytes each) of the K tile holds token s / 24, chunk kswz(s % 24);
+  // of the V tile token s / 16, chunk vswz(s % 16).
   uint32_t koff[kPKDma], voff[kPVDma];
 #pragma unroll
   for (int k = 0; k < kPKDma; ++k) {
@@ -153,37 +209,104 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const int s = (wave + k * kPWaves) * 64 + lane, t = s >> 4;
     voff[k] = (uint32_t)(t * vrow_bytes + vswz(s & 15, t) * 16);
   }
-  auto issue = [&](int n) {
-    const int t0 = n * kPTile;
+  // LDS byte offset of the ring slot of stage n >= 0 (opaque to loop strength reduction, which would
+  // otherwise keep one induction register per LDS read address)
+  auto stage_lds = [&](int n) __attribute__((always_inline)) {
+    return __builtin_amdgcn_readfirstlane((n % kPStages) * kPStageBytes);
+  };
+  // DMA groups (5 loads per wave) are issued in order; group n < nst is stage n. A pipelined step
+  // issues exactly one group, one load at a time in its slots: the next stage when it is a full
+  // one, otherwise a dummy group (page 0 of the request again, into a 1 KB scratch area of LDS),
+  // so that the slots carry no branches. Groups issued after the last stage are dummies.
+  int n_stages = 0, n_groups = 0;
+  int dma_t0 = 0, dma_pg = 0;  // token offset and page id of the step's group
+  uint32_t dma_st = 0;        // its LDS destination (stage slot or scratch)
+  bool dma_real = false;
+  const char* dma_k = kbase;
+  const char* dma_v = vbase;
+  // stage n_stages, now (tail stages, steps without the pipelined part) or in the step's slots
+  auto issue = [&](bool in_step) __attribute__((always_inline)) {
+    const bool more = n_stages < nst;
+    const int n = __builtin_amdgcn_readfirstlane(n_stages);
+    const int t0 = n * kPStage;
+    const int tlim = L - 1 - t0;
+    if (in_step && (!more || (staged && tlim >= kPStage - 1))) {
+      dma_real = more;
+      dma_t0 = more ? t0 : 0;
+      dma_st = more ? lds0 + stage_lds(n) : lds_dummy;
+      n_stages += more ? 1 : 0;
+      ++n_groups;
+      return;
+    }
+    if (in_step) {  // the request's last stage goes now, the step's slots issue a dummy group
+      dma_real = false;
+      dma_t0 = 0;
+      dma_st = lds_dummy;
+      ++n_groups;
+    }
+    if (!more) return;
+    ++n_stages;
+    ++n_groups;
     const int pid = staged ? __builtin_amdgcn_readfirstlane(s_pg[t0 >> p.log2_ps])
                            : min(max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0),
                                  p.num_pages - 1);
     const int64_t row_base = (int64_t)pid * (ps_mask + 1) + (t0 & ps_mask);
     const char* ksrc = kbase + row_base * krow_bytes;
     const char* vsrc = vbase + row_base * vrow_bytes;
-    const uint32_t st = lds0 + (n % kPStages) * kPStageBytes;
-    const int tlim = L - 1 - t0;
-    if (tlim >= kPTile - 1) {
+    const uint32_t st = lds0 + stage_lds(n);
+    if (tlim >= kPStage - 1) {
 #pragma unroll
       for (int k = 0; k < kPKDma; ++k) dma16_saddr(ksrc, koff[k], st + (wave + k * kPWaves) * 1024);
 #pragma unroll
       for (int k = 0; k < kPVDma; ++k) dma16_saddr(vsrc, voff[k], st + kPKBytes + (wave + k * kPWaves) * 1024);
-    } else {
+    } else {  // the request's last stage: rows past the last key reload the last key
+      // lane index from a volatile asm, so that these offsets are computed here and not kept in
+      // registers across the loop
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
       for (int k = 0; k < kPKDma; ++k) {
-        const int s = (wave + k * kPWaves) * 64 + lane, t = s / 24;
+        const int s = (wave + k * kPWaves) * 64 + ln, t = s / 24;
         const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes + kswz(s - 24 * t, t) * 16);
         dma16_saddr(ksrc, o, st + (wave + k * kPWaves) * 1024);
       }
 #pragma unroll
       for (int k = 0; k < kPVDma; ++k) {
-        const int s = (wave + k * kPWaves) * 64 + lane, t = s >> 4;
+        const int s = (wave + k * kPWaves) * 64 + ln, t = s >> 4;
         const uint32_t o = (uint32_t)(min(t, tlim) * vrow_bytes + vswz(s & 15, t) * 16);
         dma16_saddr(vsrc, o, st + kPKBytes + (wave + k * kPWaves) * 1024);
       }
     }
   };
-
+  // slot work of the step's group: part 0 reads the page id (in the step, so the compiler waits
+  // for that LDS read alone), parts 1..5 issue the loads
+  auto dma_part = [&](int k) __attribute__((always_inline)) {
+    if (k == 0) {
+      dma_pg = s_pg[dma_t0 >> p.log2_ps];
+      return;
+    }
+    if (k == 1) {
+      const int64_t row_base =
+          (int64_t)__builtin_amdgcn_readfirstlane(dma_pg) * (ps_mask + 1) + (dma_t0 & ps_mask);
+      dma_k = kbase + row_base * krow_bytes;
+      dma_v = vbase + row_base * vrow_bytes;
+    }
+    const int d = k - 1;
+    const uint32_t kdst = dma_real ? dma_st + (wave + d * kPWaves) * 1024 : dma_st;
+    const uint32_t vdst = dma_real ? dma_st + kPKBytes + (wave + (d - kPKDma) * kPWaves) * 1024 : dma_st;
+    if (d < kPKDma) dma16_saddr(dma_k, koff[d], kdst);
+    else dma16_saddr(dma_v, voff[d - kPKDma], vdst);
+  };
+  // stage n + 1 has landed for every wave, and every wave is done with step n - 1; the stage
+  // that step n - 1 finished with is refilled. Groups after stage n + 1's: 3 in the steady state
+  // (then at most 15 loads may stay in flight), fewer near the start and the end (then wait for
+  // all: a longer wait, never a shorter one).
+  auto step_sync = [&](int n, bool in_step) __attribute__((always_inline)) {
+    if (n_groups - 2 - n >= kPStages - 4) wait_vmcnt<kPDma * (kPStages - 4)>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    issue(in_step);
+  };
   // ---- queries: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
   bf16x8 qf[2][12];
 #pragma unroll
@@ -200,16 +323,15 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int ks = 0; ks < 12; ++ks) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
 
-  int n_issued = 0;
-  for (; n_issued < kPStages - 1 && n_issued < ntiles; ++n_issued) issue(n_issued);
+  while (n_stages < kPStages - 3 && n_stages < nst) issue(false);
 
   // ---- per-lane LDS read offsets
-  // K operand of k-step ks = 4m + r, key half kh: chunk 8m + 2r + g32 of key 32kh + c32 at k_off[r] + 128m
+  // K operand of k-step ks = 4m + r: chunk 8m + 2r + g32 of key c32 at k_off[r] + 128m
   int k_off[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) k_off[r] = c32 * kPKRowBytes + kswz(2 * r + g32, c32) * 16;
-  // V^T operand: 16-lane group gq = lane / 16 covers dims 16(gq & 1) .. +16 of a 32-dim block and the
-  // key half vh = gq >> 1; lane a16 reads token 4vh + (a16 >> 2) (+ 16 ksp + 8 second + 32 kh), dims
+  // V^T operand: 16-lane group gq = lane / 16 covers dims 16(gq & 1) .. +16 of a 32-dim block and
+  // the key quarter vh = gq >> 1; lane a16 reads token 4vh + (a16 >> 2) (+ 16 ksp + 8 second), dims
   // 4(a16 & 3) .. +4; chunk 4db + y (y < 4) is stored at (4db + y) ^ 2vt
   const int gq = lane >> 4, a16 = lane & 15, vh = gq >> 1, vt = a16 >> 2;
   int v_off[2];
@@ -219,119 +341,196 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int d = 0; d < 2; ++d) v_off[d] = (4 * vh + vt) * kPVRowBytes + ((4 * d) ^ z) * 16 + (a16 & 1) * 8;
   }
+  // K operand ks of the stage at LDS byte offset `kt`
+  auto kread = [&](int kt, int ks) __attribute__((always_inline)) {
+    return *reinterpret_cast<const MLA_LDS bf16x8*>((const MLA_LDS char*)smem + kt + k_off[ks & 3] +
+                                                   128 * (ks >> 2));
+  };
+  // V^T operand st = (32-dim block db = st / 2, 16-key step ksp = st % 2) of the stage at `kt`; its
+  // k order (keys 16ksp + 8e + 4g32 + (0..3), e = 0, 1) matches the lanes' P^T values
+  auto vop = [&](int kt, int st) __attribute__((always_inline)) {
+    const int db = st >> 1, ksp = st & 1;
+    const MLA_LDS char* base = (const MLA_LDS char*)smem + kt + kPKBytes + v_off[db & 1] + 128 * (db >> 1) +
+                               16 * ksp * kPVRowBytes;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)base);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(base + 8 * kPVRowBytes));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
 
   f32x16_t O[4][2];
 #pragma unroll
   for (int db = 0; db < 4; ++db) O[db][0] = O[db][1] = f32x16_t{};
   float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  f32x16_t sc[2][2];  // [parity][qs]: scores of the stage being softmaxed / being computed
+  u32x4 pb[2][2][2];  // [parity][qs][ksp]: bf16 numerators P^T
+  bf16x8 vb[4];       // V^T operands (the first three of a step are read by the step before)
+  bf16x8 kb[5];       // K operands in flight
 
-  for (int n = 0; n < ntiles; ++n) {
-    wait_vmcnt_dyn(kPDma * (n_issued - 1 - n));
-    barrier_lds();
-    if (n_issued < ntiles) issue(n_issued++);
-    if (n >= wave_tiles) continue;  // uniform per wave: its queries need no further keys
-
-    const MLA_LDS char* TK = (const MLA_LDS char*)smem + (n % kPStages) * kPStageBytes;
-    const MLA_LDS char* TV = TK + kPKBytes;
-    const int kfirst = n * kPTile;
-
-    // ---- S^T = K . Q^T: key halves kh x query sub-blocks qs; read r = 12kh + ks
-    f32x16_t sc[2][2];
-    {
-      auto kread = [&](int r) {
-        const int kh = r / 12, ks = r % 12;
-        return *reinterpret_cast<const MLA_LDS bf16x8*>(TK + kh * 32 * kPKRowBytes + k_off[ks & 3] + 128 * (ks >> 2));
-      };
-      bf16x8 kb[4];
+  // ---- scores of stage 0 (before the first pipelined step)
+  auto qk_plain = [&](f32x16_t (&dst)[2], int kt) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) kb[r] = kread(r);
+    for (int r = 0; r < 4; ++r) kb[r] = kread(kt, r);
 #pragma unroll
-      for (int r = 0; r < 24; ++r) {
-        const bf16x8 a = kb[r & 3];
-        if (r + 4 < 24) kb[r & 3] = kread(r + 4);
-        const int kh = r / 12, ks = r % 12;
-        if (ks == 0) {
-          mfma_qk_first(sc[kh][0], a, qf[0][0]);
-          mfma_qk_first(sc[kh][1], a, qf[1][0]);
-        } else {
-          mfma_qk(sc[kh][0], a, qf[0][ks]);
-          mfma_qk(sc[kh][1], a, qf[1][ks]);
-        }
+    for (int ks = 0; ks < 12; ++ks) {
+      const bf16x8 a = kb[ks & 3];
+      if (ks + 4 < 12) kb[ks & 3] = kread(kt, ks + 4);
+      if (ks == 0) {
+        mfma_qk_first(dst[0], a, qf[0][0]);
+        mfma_qk_first(dst[1], a, qf[1][0]);
+      } else {
+        mfma_qk(dst[0], a, qf[0][ks]);
+        mfma_qk(dst[1], a, qf[1][ks]);
       }
     }
-    mfma_result_wait(sc[0][0], sc[0][1], sc[1][0], sc[1][1]);
-
-    // ---- online softmax; lane holds keys kfirst + 32kh + 8(i/4) + 4*g32 + i%4 (i < 16) of query
-    // column c32 of sub-block qs; the scores become numerators in place
-    bf16x8 pb[2][2][2];  // [kh][qs][ksp]
+  };
+  float fr[2] = {1.0f, 1.0f};  // rescale factors of the stage just softmaxed (1: reference unchanged)
+  // causal mask of stage j's scores (stages that reach past the wave's first query); all == true
+  // masks every score
+  auto mask_scores = [&](f32x16_t (&s)[2], int j, bool all) __attribute__((always_inline)) {
+    mfma_wait_scores(s[0], s[1]);
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      const int qpos = P + row0 + 32 * qs + c32;                   // this lane's query position
-      const bool diag = kfirst + kPTile - 1 > P + row0 + 32 * qs;  // uniform: some key may follow a query
-      float m = -INFINITY;
+      // key kfirst + 8(i/4) + 4 g32 + i%4 follows query P + row0 + 32qs + c32 when
+      // 8(i/4) + i%4 > lim, lim = P + row0 + 32qs + c32 - kfirst - 4 g32
+      const int lim = all ? -1 : P + row0 + 32 * qs + c32 - j * kPStage - 4 * g32;
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
+      for (int i = 0; i < 16; ++i)
+        if (8 * (i >> 2) + (i & 3) > lim) s[qs][i] = -INFINITY;
+    }
+  };
+  // O holds the value sums up to the stage before the one just softmaxed: bring it to the new
+  // reference (rare after the first stages)
+  auto rescale = [&]() __attribute__((always_inline)) {
+    if (__ballot(fr[0] != 1.0f || fr[1] != 1.0f) != 0) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (diag && kfirst + 32 * kh + 8 * (i >> 2) + 4 * g32 + (i & 3) > qpos) sc[kh][qs][i] = -INFINITY;
-          m = fmaxf(m, sc[kh][qs][i]);
-        }
-      const float mblk = fmaxf(m, __shfl_xor(m, 32)) * p.scale_log2;
-      const bool up = mblk > m_ref[qs] + kPRescaleLog2;
-      if (__ballot(up) != 0) {  // rare after the first tiles: move the reference, rescale O and l
-        const float m_new = up ? mblk : m_ref[qs];
-        const float f = __builtin_amdgcn_exp2f(m_ref[qs] - m_new);
-        l_run[qs] *= f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) O[db][qs] *= f;
-        m_ref[qs] = m_new;
-      }
-      const float neg_m = -m_ref[qs];
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sc[kh][qs][i] = __builtin_amdgcn_exp2f(fmaf(sc[kh][qs][i], p.scale_log2, neg_m));
-          l_run[qs] += sc[kh][qs][i];
-        }
-#pragma unroll
-        for (int ksp = 0; ksp < 2; ++ksp) {
-          const f32x16_t& e = sc[kh][qs];
-          const u32x4 w{pack_bf16x2(e[8 * ksp + 0], e[8 * ksp + 1]), pack_bf16x2(e[8 * ksp + 2], e[8 * ksp + 3]),
-                        pack_bf16x2(e[8 * ksp + 4], e[8 * ksp + 5]), pack_bf16x2(e[8 * ksp + 6], e[8 * ksp + 7])};
-          pb[kh][qs][ksp] = __builtin_bit_cast(bf16x8, w);
-        }
+      for (int db = 0; db < 4; ++db) {
+        O[db][0] *= fr[0];
+        O[db][1] *= fr[1];
+        // keep O in the accumulation registers, where the value MFMAs want it
+        asm volatile("" : "+a"(O[db][0]), "+a"(O[db][1]));
       }
     }
+  };
 
-    // ---- O^T[32 dims x 32 queries] += V^T . P^T per 32-dim block db = 2pp + d; k-step (kh, ksp) covers
-    // keys 32kh + 16ksp + 4vh + (0..3) and 32kh + 16ksp + 8 + 4vh + (0..3), matching the lanes' P^T values
-    auto vread = [&](int db, int kh, int ksp, int second) {
-      const int off = v_off[db & 1] + 128 * (db >> 1) + (32 * kh + 16 * ksp + 8 * second) * kPVRowBytes;
-      return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(TV + off));
+  // ---- pipelined step j: value MFMAs of stage j - 1 (slots 0..15), score MFMAs of stage j + 1
+  // (slots 16..39), softmax of stage j spread over all slots; one MFMA per slot, the order pinned
+  // by scheduling barriers. V^T operands 0..2 come from the step before, 3..7 are read in slots
+  // 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
+  auto step_fast = [&](auto par_c, int j) __attribute__((always_inline)) {
+    constexpr int par = decltype(par_c)::value;
+    f32x16_t(&scs)[2] = sc[par];
+    f32x16_t(&scn)[2] = sc[par ^ 1];
+    u32x4(&pbw)[2][2] = pb[par];
+    const u32x4(&pbr)[2][2] = pb[par ^ 1];
+    const int kt = stage_lds(j + 1), vtile = stage_lds(j > 0 ? j - 1 : 0);
+    float mx[2], negm[2];
+    auto uop = [&](auto u_c) __attribute__((always_inline)) {
+      constexpr int u = decltype(u_c)::value;
+      if constexpr (u < 16) {
+        constexpr int qs = u >> 3, k = u & 7;
+        const float a = fmaxf(scs[qs][2 * k], scs[qs][2 * k + 1]);
+        mx[qs] = k == 0 ? a : fmaxf(mx[qs], a);
+        pin(mx[qs]);
+      } else if constexpr (u < 18) {
+        constexpr int qs = u - 16;
+        mx[qs] = max_halves(mx[qs]);
+        pin(mx[qs]);
+      } else if constexpr (u < 20) {
+        constexpr int qs = u - 18;
+        const float mblk = mx[qs] * p.scale_log2;
+        const bool up = mblk > m_ref[qs] + kPRescaleLog2;
+        fr[qs] = up ? __builtin_amdgcn_exp2f(m_ref[qs] - mblk) : 1.0f;
+        m_ref[qs] = up ? mblk : m_ref[qs];
+        l_run[qs] *= fr[qs];
+        negm[qs] = -m_ref[qs];
+        pin(fr[qs]);
+        pin(m_ref[qs]);
+        pin(l_run[qs]);
+        pin(negm[qs]);
+      } else {
+        constexpr int v = u - 20, k = v / 6, r = v % 6, qs = r / 3, rr = r % 3;
+        if constexpr (rr < 2) {
+          constexpr int i = 2 * k + rr;
+          float e = __builtin_amdgcn_exp2f(fmaf(scs[qs][i], p.scale_log2, negm[qs]));
+          pin(e);
+          scs[qs][i] = e;
+          l_run[qs] += e;
+          pin(l_run[qs]);
+        } else {
+          uint32_t w = pack_bf16x2(scs[qs][2 * k], scs[qs][2 * k + 1]);
+          pin(w);
+          pbw[qs][k >> 2][k & 3] = w;
+        }
+      }
     };
-    auto vop = [&](int st) {  // st = (db, kh, ksp)
-      const int db = st >> 2, kh = (st >> 1) & 1, ksp = st & 1;
-      return __builtin_shufflevector(vread(db, kh, ksp, 0), vread(db, kh, ksp, 1), 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    bf16x8 vb[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) vb[st] = vop(st);
-#pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const int db = st >> 2, kh = (st >> 1) & 1, ksp = st & 1;
-      const bf16x8 a = vb[st & 3];
-      if (st + 4 < 16) vb[st & 3] = vop(st + 4);
-      O[db][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kh][0][ksp], O[db][0], 0, 0, 0);
-      O[db][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kh][1][ksp], O[db][1], 0, 0, 0);
+    static_for<kSlots>([&](auto s_c) __attribute__((always_inline)) {
+      constexpr int s = decltype(s_c)::value;
+      if constexpr (s < 16) {
+        constexpr int st = s >> 1, qs = s & 1;
+        mfma_pv(O[st >> 1][qs], vb[st & 3], pbr[qs][st & 1]);
+        asm volatile("" : "+a"(O[st >> 1][qs]));  // keeps the value MFMA in its slot
+      } else {
+        constexpr int ks = (s - 16) >> 1, qs = s & 1;
+        if constexpr (ks == 0) mfma_qk_first(scn[qs], kb[0], qf[qs][0]);
+        else mfma_qk(scn[qs], kb[ks % 5], qf[qs][ks]);
+      }
+      if constexpr (s == 0) mfma_wait_scores(scs[0], scs[1]);
+      if constexpr (s == 0) dma_part(0);  // the stage refill, spread over the step
+      if constexpr (s % 8 == 3) dma_part(s / 8 + 1);
+      if constexpr (s < 10 && (s & 1) == 0) {
+        constexpr int st = (s >> 1) + 3;
+        vb[st & 3] = vop(vtile, st);
+      }
+      if constexpr (s >= 8 && s <= 30 && (s & 1) == 0) {
+        constexpr int ks = (s - 8) >> 1;
+        kb[ks % 5] = kread(kt, ks);
+      }
+      static_for<kUops>([&](auto u_c) __attribute__((always_inline)) {
+        if constexpr (uop_slot(decltype(u_c)::value) == s) uop(u_c);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    rescale();
+  };
+
+  // step j <= W of a wave: the pipelined step. At j = 0 the value pass adds zero numerators (V of
+  // stage 0, which holds finite data); at j = W - 1 the scores of stage W are computed, and at
+  // j = W fully masked, so that step W only adds the values of stage W - 1.
+  auto step = [&](auto par_c, int j) __attribute__((always_inline)) {
+    constexpr int par = decltype(par_c)::value;
+    step_sync(j, j <= W && W > 0);
+    if (j <= W && W > 0) {
+      if (j * kPStage + kPStage - 1 > P + row0) mask_scores(sc[par], j, j == W);  // uniform
+      step_fast(par_c, j);
+      if (j < W) {
+        const int t = stage_lds(j);  // V^T operands 0..2 of stage j for the next step
+        vb[0] = vop(t, 0);
+        vb[1] = vop(t, 1);
+        vb[2] = vop(t, 2);
+      }
     }
+  };
+
+  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier)
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
+  step_sync(-1, false);
+  if (W > 0) {
+    qk_plain(sc[0], stage_lds(0));
+    vb[0] = vop(stage_lds(0), 0);
+    vb[1] = vop(stage_lds(0), 1);
+    vb[2] = vop(stage_lds(0), 2);
+  }
+  for (int j = 0; j <= nst; j += 2) {
+    step(ic<0>{}, j);
+    if (j + 1 <= nst) step(ic<1>{}, j + 1);
   }
 
   // ---- finalise: lane holds query column c32 and dims 32db + 8(i/4) + 4*g32 + i%4
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
     const int row = row0 + 32 * qs + c32;
-    const float l_tot = l_run[qs] + __shfl_xor(l_run[qs], 32);
+    const float l_tot = sum_halves(l_run[qs]);
     if (row >= E || wave_rows == 0) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     __bf16* orow = p.out + (int64_t)(q0 + row) * p.out_stride_t + (int64_t)h * p.out_stride_h + 4 * g32;

@@ -91,3 +91,10 @@ def test_prefill_growing_logits_rescale():
     case.k_pool = k.to(torch.bfloat16)
     case.q[..., 0] = 8.0
     check_case(case)
+
+
+def test_prefill_prefix_beyond_staged_page_ids():
+    """More pages than the kernel stages in LDS (1024 at page size 64): the page ids are read from
+    the table per stage."""
+    case = make_prefill_case(2, 64, extends=[40, 300], prefixes=[66000, 65500], seed=14)
+    check_case(case)
