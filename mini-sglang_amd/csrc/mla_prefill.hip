@@ -18,8 +18,9 @@
 //    softmax of stage j, the two instruction streams interleaved slot by slot
 //    (one MFMA per slot). Steps that need masking (the diagonal), and the
 //    first and last steps of a wave, run the three parts one after another.
-//  * Online softmax in the log2 domain with lazy rescaling: the running max
-//    moves (and O, l are rescaled) only when a stage's max exceeds it by 8.
+//  * Online softmax in the log2 domain against a lazy row reference: the exact
+//    max of the wave's first stage, moved (with O and l rescaled, and the
+//    stage redone) only when a stage's numerators sum past 2^32.
 //  * The heads of one (request, query block) are consecutive CTAs, so the
 //    query blocks of one head are 'heads' CTAs apart and, with heads a
 //    multiple of 8, land on the same XCD and share its L2 for K/V.
@@ -45,19 +46,16 @@ constexpr int kPStages = 7;
 constexpr int kPKDma = kPKBytes / 1024 / kPWaves;  // 3 wave-wide DMA loads per wave
 constexpr int kPVDma = kPVBytes / 1024 / kPWaves;  // 2
 constexpr int kPDma = kPKDma + kPVDma;             // 5
-constexpr float kPRescaleLog2 = 8.0f;
 constexpr int kPMaxPages = 1024;  // page ids of a CTA's keys staged in LDS (else read per stage)
 
 // ---- the softmax of one stage as a list of micro-operations, spread over the 40 MFMA slots of a
-// pipelined step in proportion to their cost (4-cycle units; exp2 is a quarter-rate instruction):
-//   u in [0, 16): running max over two scores (sub-block u / 8)
-//   u in [16, 18): max across the two wave halves
-//   u in [18, 20): reference update, rescale factor, -m
-//   u in [20, 68): v = u - 20, k = v / 6, r = v % 6, sub-block r / 3: r % 3 < 2 -> exp2 of score
-//                  2k + r % 3 and its sum; r % 3 == 2 -> pack scores 2k, 2k + 1 to bf16
+// pipelined step in proportion to their cost (half-instruction units; next to running MFMAs a
+// vector instruction costs ~8 cycles and exp2 ~11). For u in [0, 48): k = u / 6, r = u % 6,
+// sub-block r / 3: r % 3 < 2 -> exp2 of score 2k + r % 3 against the row's reference and its
+// sum; r % 3 == 2 -> pack scores 2k, 2k + 1 to bf16.
 constexpr int kSlots = 40;  // 16 value MFMAs + 24 score MFMAs
-constexpr int kUops = 68;
-constexpr int uop_weight(int u) { return u < 16 ? 1 : u < 18 ? 2 : u < 20 ? 10 : ((u - 20) % 3 == 2 ? 1 : 6); }
+constexpr int kUops = 48;
+constexpr int uop_weight(int u) { return u % 3 == 2 ? 2 : 7; }
 constexpr int uop_total() {
   int t = 0;
   for (int u = 0; u < kUops; ++u) t += uop_weight(u);
@@ -68,6 +66,11 @@ constexpr int uop_slot(int u) {
   for (int v = 0; v < u; ++v) t += uop_weight(v);
   return t * kSlots / uop_total();
 }
+// The row reference m (log2 domain) is the exact max of the wave's first stage and moves only when
+// a stage's numerators sum past 2^32 (a score 32 above m, in log2 units) or overflow: then that
+// stage is redone against its exact max. fp32 keeps its relative precision at any scale, so the
+// lagging reference costs no accuracy.
+constexpr float kPLazyMax = 4294967296.0f;
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -383,11 +386,10 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
       }
     }
   };
-  float fr[2] = {1.0f, 1.0f};  // rescale factors of the stage just softmaxed (1: reference unchanged)
   // causal mask of stage j's scores (stages that reach past the wave's first query); all == true
   // masks every score
-  auto mask_scores = [&](f32x16_t (&s)[2], int j, bool all) __attribute__((always_inline)) {
-    mfma_wait_scores(s[0], s[1]);
+  auto mask_scores = [&](f32x16_t (&sv)[2], int j, bool all) __attribute__((always_inline)) {
+    mfma_wait_scores(sv[0], sv[1]);
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       // key kfirst + 8(i/4) + 4 g32 + i%4 follows query P + row0 + 32qs + c32 when
@@ -395,21 +397,56 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
       const int lim = all ? -1 : P + row0 + 32 * qs + c32 - j * kPStage - 4 * g32;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        if (8 * (i >> 2) + (i & 3) > lim) s[qs][i] = -INFINITY;
+        if (8 * (i >> 2) + (i & 3) > lim) sv[qs][i] = -INFINITY;
     }
   };
-  // O holds the value sums up to the stage before the one just softmaxed: bring it to the new
-  // reference (rare after the first stages)
-  auto rescale = [&]() __attribute__((always_inline)) {
-    if (__ballot(fr[0] != 1.0f || fr[1] != 1.0f) != 0) {
+  float negm[2] = {0.f, 0.f};  // -reference per sub-block (log2 domain)
+  // reference of the wave's first stage: its exact row max
+  auto init_ref = [&](f32x16_t (&sv)[2]) __attribute__((always_inline)) {
+    mfma_wait_scores(sv[0], sv[1]);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        O[db][0] *= fr[0];
-        O[db][1] *= fr[1];
-        // keep O in the accumulation registers, where the value MFMAs want it
-        asm volatile("" : "+a"(O[db][0]), "+a"(O[db][1]));
-      }
+    for (int qs = 0; qs < 2; ++qs) {
+      float m = sv[qs][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) m = fmaxf(m, sv[qs][i]);
+      m_ref[qs] = max_halves(m) * p.scale_log2;
+      negm[qs] = -m_ref[qs];
     }
+  };
+  // stage j again, its reference raised to its exact max (rare): from its raw (masked) scores,
+  // which the pipelined step keeps; O and l (which hold the stages before it) rescaled; numerators
+  // and their sum redone
+  auto redo_stage = [&](f32x16_t (&sv)[2], u32x4 (&dst)[2][2], float (&l_step)[2]) __attribute__((always_inline)) {
+    float fr[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      float m = sv[qs][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) m = fmaxf(m, sv[qs][i]);
+      const float m_new = fmaxf(max_halves(m) * p.scale_log2, m_ref[qs]);
+      fr[qs] = __builtin_amdgcn_exp2f(m_ref[qs] - m_new);
+      m_ref[qs] = m_new;
+      negm[qs] = -m_new;
+      l_run[qs] *= fr[qs];
+      float l = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[qs][2 * k], p.scale_log2, negm[qs]));
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[qs][2 * k + 1], p.scale_log2, negm[qs]));
+        l += e0 + e1;
+        dst[qs][k >> 2][k & 3] = pack_bf16x2(e0, e1);
+      }
+      l_step[qs] = l;
+    }
+    // one 16-value block at a time, so that the copies out of the accumulation registers stay few
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        O[db][qs] *= fr[qs];
+        asm volatile("" : "+a"(O[db][qs]));  // O stays in the accumulation registers
+        __builtin_amdgcn_sched_barrier(0);
+      }
   };
 
   // ---- pipelined step j: value MFMAs of stage j - 1 (slots 0..15), score MFMAs of stage j + 1
@@ -423,44 +460,21 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     u32x4(&pbw)[2][2] = pb[par];
     const u32x4(&pbr)[2][2] = pb[par ^ 1];
     const int kt = stage_lds(j + 1), vtile = stage_lds(j > 0 ? j - 1 : 0);
-    float mx[2], negm[2];
+    float l_step[2], ev[2][2];  // ev: the numerators of the pair being packed (raw scores stay)
     auto uop = [&](auto u_c) __attribute__((always_inline)) {
       constexpr int u = decltype(u_c)::value;
-      if constexpr (u < 16) {
-        constexpr int qs = u >> 3, k = u & 7;
-        const float a = fmaxf(scs[qs][2 * k], scs[qs][2 * k + 1]);
-        mx[qs] = k == 0 ? a : fmaxf(mx[qs], a);
-        pin(mx[qs]);
-      } else if constexpr (u < 18) {
-        constexpr int qs = u - 16;
-        mx[qs] = max_halves(mx[qs]);
-        pin(mx[qs]);
-      } else if constexpr (u < 20) {
-        constexpr int qs = u - 18;
-        const float mblk = mx[qs] * p.scale_log2;
-        const bool up = mblk > m_ref[qs] + kPRescaleLog2;
-        fr[qs] = up ? __builtin_amdgcn_exp2f(m_ref[qs] - mblk) : 1.0f;
-        m_ref[qs] = up ? mblk : m_ref[qs];
-        l_run[qs] *= fr[qs];
-        negm[qs] = -m_ref[qs];
-        pin(fr[qs]);
-        pin(m_ref[qs]);
-        pin(l_run[qs]);
-        pin(negm[qs]);
+      constexpr int k = u / 6, r = u % 6, qs = r / 3, rr = r % 3;
+      if constexpr (rr < 2) {
+        constexpr int i = 2 * k + rr;
+        float e = __builtin_amdgcn_exp2f(fmaf(scs[qs][i], p.scale_log2, negm[qs]));
+        pin(e);
+        ev[qs][rr] = e;
+        l_step[qs] = i == 0 ? e : l_step[qs] + e;
+        pin(l_step[qs]);
       } else {
-        constexpr int v = u - 20, k = v / 6, r = v % 6, qs = r / 3, rr = r % 3;
-        if constexpr (rr < 2) {
-          constexpr int i = 2 * k + rr;
-          float e = __builtin_amdgcn_exp2f(fmaf(scs[qs][i], p.scale_log2, negm[qs]));
-          pin(e);
-          scs[qs][i] = e;
-          l_run[qs] += e;
-          pin(l_run[qs]);
-        } else {
-          uint32_t w = pack_bf16x2(scs[qs][2 * k], scs[qs][2 * k + 1]);
-          pin(w);
-          pbw[qs][k >> 2][k & 3] = w;
-        }
+        uint32_t w = pack_bf16x2(ev[qs][0], ev[qs][1]);
+        pin(w);
+        pbw[qs][k >> 2][k & 3] = w;
       }
     };
     static_for<kSlots>([&](auto s_c) __attribute__((always_inline)) {
@@ -490,7 +504,9 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    rescale();
+    if (__ballot(!(l_step[0] < kPLazyMax) || !(l_step[1] < kPLazyMax)) != 0) redo_stage(scs, pbw, l_step);
+    l_run[0] += l_step[0];
+    l_run[1] += l_step[1];
   };
 
   // step j <= W of a wave: the pipelined step. At j = 0 the value pass adds zero numerators (V of
@@ -501,6 +517,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     step_sync(j, j <= W && W > 0);
     if (j <= W && W > 0) {
       if (j * kPStage + kPStage - 1 > P + row0) mask_scores(sc[par], j, j == W);  // uniform
+      if (j == 0) init_ref(sc[par]);
       step_fast(par_c, j);
       if (j < W) {
         const int t = stage_lds(j);  // V^T operands 0..2 of stage j for the next step

@@ -98,3 +98,30 @@ def test_prefill_prefix_beyond_staged_page_ids():
     the table per stage."""
     case = make_prefill_case(2, 64, extends=[40, 300], prefixes=[66000, 65500], seed=14)
     check_case(case)
+
+
+def _set_key_dim0(case, fn):
+    """k[..., 0] of every head := fn(logical token index, request length), in each request's order."""
+    k = case.k_pool.float()
+    ps = case.page_size
+    for b, L in enumerate(case.seq_lens_k.tolist()):
+        rows = R.token_rows(case.page_table[b].cpu(), L, ps)
+        t = torch.arange(L, dtype=torch.float32)
+        k.view(-1, *k.shape[2:])[rows, :, 0] = fn(t, L).unsqueeze(1)
+    case.k_pool = k.to(torch.bfloat16)
+
+
+def test_prefill_reference_moves_along_keys():
+    """Scores that climb ~50 (log2 units) along the keys: the row reference has to move."""
+    case = make_prefill_case(2, 64, extends=[300, 77], prefixes=[1500, 400], seed=15)
+    _set_key_dim0(case, lambda t, L: 60.0 * t / L)
+    case.q[..., 0] = 8.0
+    check_case(case)
+
+
+def test_prefill_single_dominant_key():
+    """One key scores ~200 above the rest, in the middle of the prefix."""
+    case = make_prefill_case(4, 64, extends=[200], prefixes=[900], seed=16)
+    _set_key_dim0(case, lambda t, L: torch.where(t == 517, 240.0, 0.0))
+    case.q[..., 0] = 8.0
+    check_case(case)
