@@ -212,51 +212,32 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const int s = (wave + k * kPWaves) * 64 + lane, t = s >> 4;
     voff[k] = (uint32_t)(t * vrow_bytes + vswz(s & 15, t) * 16);
   }
-  // LDS byte offset of the ring slot of stage n >= 0 (opaque to loop strength reduction, which would
-  // otherwise keep one induction register per LDS read address)
-  auto stage_lds = [&](int n) __attribute__((always_inline)) {
-    return __builtin_amdgcn_readfirstlane((n % kPStages) * kPStageBytes);
-  };
-  // DMA groups (5 loads per wave) are issued in order; group n < nst is stage n. A pipelined step
-  // issues exactly one group, one load at a time in its slots: the next stage when it is a full
-  // one, otherwise a dummy group (page 0 of the request again, into a 1 KB scratch area of LDS),
-  // so that the slots carry no branches. Groups issued after the last stage are dummies.
+  // DMA groups (5 loads per wave) are issued in order; real stages in stage order, a dummy group
+  // never ahead of a real stage. A pipelined step issues exactly one group, one load at a time in
+  // its slots: the next stage when it is a full one with a staged page id, otherwise a dummy group
+  // (page 0 of the request again, into a 1 KB scratch area of LDS), so that the slots carry no
+  // branches; tail stages (and unstaged page ids) are issued at once, ahead of that dummy.
   int n_stages = 0, n_groups = 0;
+  uint32_t slot_issue = 0;  // ring offset of stage n_stages
+  const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
   int dma_t0 = 0, dma_pg = 0;  // token offset and page id of the step's group
   uint32_t dma_st = 0;        // its LDS destination (stage slot or scratch)
   bool dma_real = false;
   const char* dma_k = kbase;
   const char* dma_v = vbase;
-  // stage n_stages, now (tail stages, steps without the pipelined part) or in the step's slots
-  auto issue = [&](bool in_step) __attribute__((always_inline)) {
-    const bool more = n_stages < nst;
-    const int n = __builtin_amdgcn_readfirstlane(n_stages);
-    const int t0 = n * kPStage;
+  auto next_slot = [&](uint32_t o) __attribute__((always_inline)) {
+    return o + kPStageBytes == kPStages * kPStageBytes ? 0u : o + kPStageBytes;
+  };
+  auto issue_now = [&]() __attribute__((always_inline)) {  // stage n_stages < nst, all loads now
+    const int t0 = n_stages * kPStage;
     const int tlim = L - 1 - t0;
-    if (in_step && (!more || (staged && tlim >= kPStage - 1))) {
-      dma_real = more;
-      dma_t0 = more ? t0 : 0;
-      dma_st = more ? lds0 + stage_lds(n) : lds_dummy;
-      n_stages += more ? 1 : 0;
-      ++n_groups;
-      return;
-    }
-    if (in_step) {  // the request's last stage goes now, the step's slots issue a dummy group
-      dma_real = false;
-      dma_t0 = 0;
-      dma_st = lds_dummy;
-      ++n_groups;
-    }
-    if (!more) return;
-    ++n_stages;
-    ++n_groups;
     const int pid = staged ? __builtin_amdgcn_readfirstlane(s_pg[t0 >> p.log2_ps])
                            : min(max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0),
                                  p.num_pages - 1);
     const int64_t row_base = (int64_t)pid * (ps_mask + 1) + (t0 & ps_mask);
     const char* ksrc = kbase + row_base * krow_bytes;
     const char* vsrc = vbase + row_base * vrow_bytes;
-    const uint32_t st = lds0 + stage_lds(n);
+    const uint32_t st = lds0 + slot_issue;
     if (tlim >= kPStage - 1) {
 #pragma unroll
       for (int k = 0; k < kPKDma; ++k) dma16_saddr(ksrc, koff[k], st + (wave + k * kPWaves) * 1024);
@@ -280,6 +261,27 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         dma16_saddr(vsrc, o, st + kPKBytes + (wave + k * kPWaves) * 1024);
       }
     }
+    ++n_stages;
+    ++n_groups;
+    slot_issue = next_slot(slot_issue);
+  };
+  auto issue = [&](bool in_step) __attribute__((always_inline)) {
+    if (in_step) {
+      if (__builtin_expect(n_stages < n_defer, 1)) {
+        dma_real = true;
+        dma_t0 = n_stages * kPStage;
+        dma_st = lds0 + slot_issue;
+        ++n_stages;
+        ++n_groups;
+        slot_issue = next_slot(slot_issue);
+        return;
+      }
+      dma_real = false;
+      dma_t0 = 0;
+      dma_st = lds_dummy;
+    }
+    if (n_stages < nst) issue_now();
+    if (in_step) ++n_groups;  // the dummy group, issued in the step's slots after any stage above
   };
   // slot work of the step's group: part 0 reads the page id (in the step, so the compiler waits
   // for that LDS read alone), parts 1..5 issue the loads
@@ -451,15 +453,17 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 
   // ---- pipelined step j: value MFMAs of stage j - 1 (slots 0..15), score MFMAs of stage j + 1
   // (slots 16..39), softmax of stage j spread over all slots; one MFMA per slot, the order pinned
-  // by scheduling barriers. V^T operands 0..2 come from the step before, 3..7 are read in slots
-  // 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
-  auto step_fast = [&](auto par_c, int j) __attribute__((always_inline)) {
+  // by scheduling barriers. V^T operands 0..2 are read by the step before (slots 36..38), 3..7 in
+  // slots 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
+  // ring offsets of stages j - 1 (j for j = 0), j and j + 1
+  uint32_t slot_prev = 0, slot_cur = 0, slot_next = next_slot(0);
+  auto step_fast = [&](auto par_c) __attribute__((always_inline)) {
     constexpr int par = decltype(par_c)::value;
     f32x16_t(&scs)[2] = sc[par];
     f32x16_t(&scn)[2] = sc[par ^ 1];
     u32x4(&pbw)[2][2] = pb[par];
     const u32x4(&pbr)[2][2] = pb[par ^ 1];
-    const int kt = stage_lds(j + 1), vtile = stage_lds(j > 0 ? j - 1 : 0);
+    const int kt = slot_next, vtile = slot_prev;
     float l_step[2], ev[2][2];  // ev: the numerators of the pair being packed (raw scores stay)
     auto uop = [&](auto u_c) __attribute__((always_inline)) {
       constexpr int u = decltype(u_c)::value;
@@ -499,6 +503,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         constexpr int ks = (s - 8) >> 1;
         kb[ks % 5] = kread(kt, ks);
       }
+      if constexpr (s >= 36 && s <= 38) vb[s - 36] = vop(slot_cur, s - 36);  // for the next step
       static_for<kUops>([&](auto u_c) __attribute__((always_inline)) {
         if constexpr (uop_slot(decltype(u_c)::value) == s) uop(u_c);
       });
@@ -512,31 +517,31 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // step j <= W of a wave: the pipelined step. At j = 0 the value pass adds zero numerators (V of
   // stage 0, which holds finite data); at j = W - 1 the scores of stage W are computed, and at
   // j = W fully masked, so that step W only adds the values of stage W - 1.
+  const int j_diag = (P + row0 + 1) >> 5;  // first stage that reaches past the wave's first query
   auto step = [&](auto par_c, int j) __attribute__((always_inline)) {
     constexpr int par = decltype(par_c)::value;
-    step_sync(j, j <= W && W > 0);
-    if (j <= W && W > 0) {
-      if (j * kPStage + kPStage - 1 > P + row0) mask_scores(sc[par], j, j == W);  // uniform
-      if (j == 0) init_ref(sc[par]);
-      step_fast(par_c, j);
-      if (j < W) {
-        const int t = stage_lds(j);  // V^T operands 0..2 of stage j for the next step
-        vb[0] = vop(t, 0);
-        vb[1] = vop(t, 1);
-        vb[2] = vop(t, 2);
-      }
+    const bool work = j <= W && W > 0;
+    step_sync(j, work);
+    if (work) {
+      if (__builtin_expect(j >= j_diag, 0)) mask_scores(sc[par], j, j == W);
+      if (__builtin_expect(j == 0, 0)) init_ref(sc[par]);
+      step_fast(par_c);
     }
+    slot_prev = slot_cur;
+    slot_cur = slot_next;
+    slot_next = next_slot(slot_next);
   };
 
-  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier)
+  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier). A wave
+  // without rows has W = 0 and only takes the barriers: its "step 0" work is skipped below.
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
   step_sync(-1, false);
   if (W > 0) {
-    qk_plain(sc[0], stage_lds(0));
-    vb[0] = vop(stage_lds(0), 0);
-    vb[1] = vop(stage_lds(0), 1);
-    vb[2] = vop(stage_lds(0), 2);
+    qk_plain(sc[0], 0);
+    vb[0] = vop(0, 0);
+    vb[1] = vop(0, 1);
+    vb[2] = vop(0, 2);
   }
   for (int j = 0; j <= nst; j += 2) {
     step(ic<0>{}, j);
