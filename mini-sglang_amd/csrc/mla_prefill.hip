@@ -49,13 +49,14 @@ constexpr int kPDma = kPKDma + kPVDma;             // 5
 constexpr int kPMaxPages = 1024;  // page ids of a CTA's keys staged in LDS (else read per stage)
 
 // ---- the softmax of one stage as a list of micro-operations, spread over the 40 MFMA slots of a
-// pipelined step in proportion to their cost (half-instruction units; next to running MFMAs a
-// vector instruction costs ~8 cycles and exp2 ~11). For u in [0, 48): k = u / 6, r = u % 6,
-// sub-block r / 3: r % 3 < 2 -> exp2 of score 2k + r % 3 against the row's reference and its
-// sum; r % 3 == 2 -> pack scores 2k, 2k + 1 to bf16.
+// pipelined step in proportion to their cost (~4-cycle units; next to running MFMAs a vector
+// instruction costs ~8 cycles and exp2 ~11). For u in [0, 48): k = u / 6, r = u % 6:
+//   r = 0, 1 -> exp2 of score 2k + r of sub-block 0 against the row reference; r = 2, 3 -> the
+//   same for sub-block 1; r = 4, 5 -> sub-block r - 4: add the pair to the row sum and pack it to
+//   bf16. No exp2 result is used by the next instruction (that would cost a wait state).
 constexpr int kSlots = 40;  // 16 value MFMAs + 24 score MFMAs
 constexpr int kUops = 48;
-constexpr int uop_weight(int u) { return u % 3 == 2 ? 2 : 7; }
+constexpr int uop_weight(int u) { return u % 6 < 4 ? 5 : 6; }
 constexpr int uop_total() {
   int t = 0;
   for (int u = 0; u < kUops; ++u) t += uop_weight(u);
@@ -467,16 +468,16 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     float l_step[2], ev[2][2];  // ev: the numerators of the pair being packed (raw scores stay)
     auto uop = [&](auto u_c) __attribute__((always_inline)) {
       constexpr int u = decltype(u_c)::value;
-      constexpr int k = u / 6, r = u % 6, qs = r / 3, rr = r % 3;
-      if constexpr (rr < 2) {
-        constexpr int i = 2 * k + rr;
-        float e = __builtin_amdgcn_exp2f(fmaf(scs[qs][i], p.scale_log2, negm[qs]));
-        pin(e);
-        ev[qs][rr] = e;
-        l_step[qs] = i == 0 ? e : l_step[qs] + e;
-        pin(l_step[qs]);
+      constexpr int k = u / 6, r = u % 6;
+      if constexpr (r < 4) {
+        constexpr int qs = r >> 1, e = r & 1;
+        ev[qs][e] = __builtin_amdgcn_exp2f(fmaf(scs[qs][2 * k + e], p.scale_log2, negm[qs]));
+        pin(ev[qs][e]);
       } else {
+        constexpr int qs = r - 4;
+        l_step[qs] = k == 0 ? ev[qs][0] + ev[qs][1] : l_step[qs] + ev[qs][0] + ev[qs][1];
         uint32_t w = pack_bf16x2(ev[qs][0], ev[qs][1]);
+        pin(l_step[qs]);
         pin(w);
         pbw[qs][k >> 2][k & 3] = w;
       }
