@@ -2,11 +2,13 @@
 // (the Kimi-K2 / DeepSeek-V3 decode shape on one GPU).
 //
 // Same plan, workspace and outputs as mla_decode_kernel, different schedule:
-//  * The CTA's whole (request, token) range is ONE stream of 32-token tiles:
-//    the 4-stage LDS ring keeps prefetching across piece boundaries, so a new
-//    piece costs one query load instead of a drained-and-refilled ring. The
-//    page id of every tile and the bounds of every request of the range are
-//    staged in LDS once, at CTA start.
+//  * The CTA's whole (request, token) range is ONE stream of 32-row tiles:
+//    per piece, two tiles of queries (heads 0..31, 32..63: a query row has the
+//    latent row's 576 dims, so it is staged like a KV row) and then the
+//    piece's 32-token KV tiles. The 4-stage LDS ring keeps prefetching across
+//    piece boundaries, queries included, so a new piece never drains it. The
+//    page id of every KV tile and the bounds of every request of the range
+//    are staged in LDS once, at CTA start.
 //  * 4 waves = 2 head groups (32 heads each) x 2 halves. Wave (hg, th):
 //      S^T[16 tokens (half th) x 32 heads] = K . Q^T     36 MFMAs, 18 K reads
 //      softmax numerators of those 16 tokens, exchanged with the partner
@@ -30,9 +32,10 @@ constexpr int kSKPrefetch = 6;             // K operands in flight
 constexpr int kSVPrefetch = 4;             // V operand pairs in flight
 constexpr float kSOverflowLog2 = 64.0f;    // see mla_decode.hip
 
-// Position in the CTA's stream: request rb + r, tile start t, piece [t0, t1).
+// Position in the CTA's stream: request rb + r, piece [t0, t1); q < 2: the piece's query tile q
+// (heads 32q .. +32), q == 2: the KV tile starting at token t.
 struct Cursor {
-  int r, t, t0, t1;
+  int r, t, t0, t1, q;
 };
 
 __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeParams p) {
@@ -147,20 +150,42 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
       const int t0 = __builtin_amdgcn_readfirstlane(s_t0[r]);
       const int t1 = __builtin_amdgcn_readfirstlane(s_t1[r]);
       if (t1 > t0) {
-        cur = Cursor{r, t0, t0, t1};
+        cur = Cursor{r, t0, t0, t1, 0};
         return true;
       }
     }
     return false;
   };
   auto advance = [&](Cursor& cur) -> bool {
+    if (cur.q < 2) {
+      ++cur.q;
+      return true;
+    }
     cur.t += kTile;
     return cur.t < cur.t1 ? true : seek(cur, cur.r + 1);
   };
+  int iss_kv = 0;  // KV tiles issued (index into s_pid)
   auto issue = [&](const Cursor& cur, int n) {  // DMA stream tile n (at cur) into ring stage n % kStages
-    const int pid = __builtin_amdgcn_readfirstlane(s_pid[min(n, 2 * kMaxCtaBlocks - 1)]);
-    const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (cur.t & ps_mask)) * row_bytes;
     const uint32_t lds_stage = lds_ring + (n % kStages) * kTileBytes;
+    if (cur.q < 2) {  // query rows 32q .. +32 of request rb + r, staged like KV rows
+      const int qrow_bytes = (int)(p.q_stride_h * 2);
+      const char* qsrc = reinterpret_cast<const char*>(p.q) + ((int64_t)(rb + cur.r) * p.q_stride_b +
+                                                             (int64_t)(32 * cur.q) * p.q_stride_h) * 2;
+      // lane index from a volatile asm, so that these offsets are computed here and not kept in
+      // registers across the loop
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+#pragma unroll
+      for (int k = 0; k < kSDma; ++k) {
+        const int s = (wave + k * kSWaves) * 64 + ln;
+        const int t = (s * 7282) >> 19;  // s / 72
+        const uint32_t voff = t * qrow_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4);
+        dma16_saddr(qsrc, voff, lds_stage + (wave + k * kSWaves) * 1024);
+      }
+      return;
+    }
+    const int pid = __builtin_amdgcn_readfirstlane(s_pid[min(iss_kv++, 2 * kMaxCtaBlocks - 1)]);
+    const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (cur.t & ps_mask)) * row_bytes;
     const int tlim = cur.t1 - 1 - cur.t;  // loads clamp to the piece's last token
     if (tlim >= kTile - 1) {
 #pragma unroll
@@ -180,23 +205,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   if (!seek(comp, 0)) return;  // uniform: every piece of the range is empty
   Cursor iss = comp;
 
-  // ---- queries of the current piece: qf[hb][ks] = head 32hg+16hb+c, dims 32ks + 8g .. +8
+  // ---- queries of the current piece: qf[hb][ks] = head 32hg+16hb+c, dims 32ks + 8g .. +8, read from
+  // the piece's query tile hg
   bf16x8 qf[2][18];
-  auto load_q = [&](int b) {
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      const __bf16* qrow =
-          p.q + (int64_t)b * p.q_stride_b + (int64_t)(32 * hg + 16 * hb + c) * p.q_stride_h + g * 8;
-#pragma unroll
-      for (int ks = 0; ks < 18; ++ks) qf[hb][ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
-    }
-    // consume: the compiler's wait for these loads lands here, outside the tile loop
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-      for (int ks = 0; ks < 18; ++ks) asm volatile("" ::"v"(qf[hb][ks]));
-  };
-  load_q(rb + comp.r);
 
   int n_issued = 0;
   bool iss_valid = true;
@@ -213,22 +224,53 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   float m_ref[2] = {0.f, 0.f}, m_max[2], l_run[2];
   bool overflow = false;
   int attempt = 0;
-  bool piece_start = true, need_q = false;
-  Cursor piece_cur = comp;
-  int piece_j = 0;
+  bool piece_start = true;
+  Cursor piece_cur = comp;  // first KV tile of the piece (set when the stream reaches it)
+  int piece_j = 0, piece_kv = 0, comp_kv = 0;  // stream / KV tile indices of it; KV tiles computed
   int st1 = 0, st2 = 0, st3 = 0;  // output stores issued 1, 2 and 3 iterations ago
 
   for (int j = 0;;) {
+    if (comp.q < 2) {
+      // a piece starts: its two query tiles (stream tiles j, j + 1). Wave (hg, th) takes the queries
+      // of head group hg from tile j + hg once both have landed; the stage of tile j is refilled by
+      // the DMA issued right after, so a barrier separates every wave's reads from that issue.
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        wait_vmcnt_dyn(kSDma * (n_issued - 1 - j) + st1 + st2 + st3);
+        barrier_lds();
+        st3 = st2;
+        st2 = st1;
+        st1 = 0;
+        if (qt == 1) {
+          const MLA_LDS char* QT = (const MLA_LDS char*)smem + ((j - 1 + hg) % kStages) * kTileBytes;
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int ks = 0; ks < 18; ++ks) {
+              const int off =
+                  ((ks & 1) ? k_off_odd : k_off_even) + 128 * (ks >> 1) + (16 * hb - 16 * th) * kRowBytes;
+              qf[hb][ks] = *reinterpret_cast<const MLA_LDS bf16x8*>(QT + off);
+            }
+          // every wave's reads of tile j - 1 complete before any wave's next DMA overwrites its stage
+          barrier_lds();
+        }
+        if (iss_valid) {
+          issue(iss, n_issued++);
+          iss_valid = advance(iss);
+        }
+        ++j;
+        advance(comp);
+      }
+      piece_cur = comp;  // the piece's first KV tile
+      piece_j = j;
+      piece_kv = comp_kv;
+    }
     // tile j's DMA is complete once at most (loads issued after it + stores since) remain
     wait_vmcnt_dyn(kSDma * (n_issued - 1 - j) + st1 + st2 + st3);
     barrier_lds();
     st3 = st2;
     st2 = st1;
     st1 = 0;
-    if (need_q) {  // first tile of a new piece: its queries (waited for right here)
-      load_q(rb + comp.r);
-      need_q = false;
-    }
     if (iss_valid) {
       issue(iss, n_issued++);
       iss_valid = advance(iss);
@@ -369,6 +411,8 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
         iss = piece_cur;
         j = piece_j;
         n_issued = piece_j;
+        iss_kv = piece_kv;
+        comp_kv = piece_kv;
         iss_valid = true;
         st1 = st2 = st3 = 0;
         attempt = 1;
@@ -421,13 +465,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     }
 
     ++j;
+    ++comp_kv;
     if (!advance(comp)) break;
-    if (piece_end) {
-      piece_start = true;
-      need_q = true;
-      piece_cur = comp;
-      piece_j = j;
-    }
+    if (piece_end) piece_start = true;
   }
 }
 
