@@ -32,6 +32,18 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "mini-sglang_amd")]
 
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mla_decode_kimi_k2_b64_traffic.md")
+PREFILL_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mla_prefill_b4_e2048_kernel_trace.md")
+
+
+def _committed_traffic(path):
+    """HBM bytes per launch (copy-calibrated FETCH_SIZE + WRITE_SIZE) from a committed counter summary."""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
 
 
 def _decode_workload(device, seed):
@@ -185,12 +197,7 @@ def bench_decode(args):
     alg_bytes = case.algorithmic_bytes()
     value_tbps = alg_bytes / (step_ms * 1e-3) / 1e12
     achieved = alg_bytes / (split_ms * 1e-3) / 1e9
-    traffic = None  # HBM bytes per decode-kernel launch from the committed counter summary
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            for line in f:
-                if line.startswith("hbm_bytes_per_launch:"):
-                    traffic = int(line.split(":")[1])
+    traffic = _committed_traffic(TRAFFIC_FILE)
     result = {
         "metric": "MLA decode achieved HBM TB/s + us/layer, Kimi-K2 shape, 1 MI355X",
         "value": round(value_tbps, 4),
@@ -264,9 +271,9 @@ def bench_prefill(args):
         lib.mla_prefill(case.q, case.k_pool, case.v_pool, case.page_table, case.cu_seqlens_q, case.seq_lens_k,
                         scale, out, lse, stream=stream)
 
-    steps = max(1, args.steps // 5)
+    steps = max(1, args.steps // 2)
     with torch.cuda.stream(stream):
-        for _ in range(max(1, args.warmup // 5)):
+        for _ in range(max(1, args.warmup // 2)):
             layer()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -289,7 +296,8 @@ def bench_prefill(args):
         "tokens_per_s": round(T / (step_ms * 1e-3), 1),
         "tflops": round(achieved, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": _committed_traffic(PREFILL_TRAFFIC_FILE)},
         "algorithmic_flops": flops,
     }
 
