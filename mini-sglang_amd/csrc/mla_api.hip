@@ -389,8 +389,9 @@ int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
       v_row_stride < (int64_t)heads * mla::kPrefillVDim)
     return fail(MLA_ERR_INVALID_ARG, "%s: k/v row strides (%lld, %lld) must be multiples of 8 and hold %d heads", who,
                 (long long)k_row_stride, (long long)v_row_stride, heads);
-  if ((int64_t)31 * k_row_stride * 2 + 384 > (int64_t)UINT32_MAX || (int64_t)31 * v_row_stride * 2 + 256 > (int64_t)UINT32_MAX)
-    return fail(MLA_ERR_UNSUPPORTED, "%s: k/v row strides too large", who);
+  if ((int64_t)page_size * k_row_stride * 2 > (int64_t)UINT32_MAX ||
+      (int64_t)page_size * v_row_stride * 2 > (int64_t)UINT32_MAX)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: one page of k/v rows exceeds 4 GiB", who);
   if (out_stride_t % 4 || out_stride_h % 4 || out_stride_h < mla::kPrefillVDim)
     return fail(MLA_ERR_INVALID_ARG, "%s: out strides (%lld, %lld) must be multiples of 4 with head stride >= 128",
                 who, (long long)out_stride_t, (long long)out_stride_h);

@@ -190,6 +190,13 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * kPKRowBytes;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * kPVRowBytes;
   const int krow_bytes = (int)(p.k_row_stride * 2), vrow_bytes = (int)(p.v_row_stride * 2);
+  // bytes of one page of K / V rows (< 4 GiB, checked by the host)
+  const uint32_t kpage_bytes = (uint32_t)krow_bytes << p.log2_ps, vpage_bytes = (uint32_t)vrow_bytes << p.log2_ps;
+  // first source row of the stage that starts at token t0, on page pid
+  auto stage_src = [&](const char* base, uint32_t pid, int t0, uint32_t page_bytes, int row_bytes)
+                       __attribute__((always_inline)) {
+    return base + ((uint64_t)pid * page_bytes + (uint32_t)((t0 & ps_mask) * row_bytes));
+  };
 
   // ---- page ids of the CTA's keys
   const int npages = __builtin_amdgcn_readfirstlane((nkeys + ps_mask) >> p.log2_ps);
@@ -235,9 +242,8 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const int pid = staged ? __builtin_amdgcn_readfirstlane(s_pg[t0 >> p.log2_ps])
                            : min(max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0),
                                  p.num_pages - 1);
-    const int64_t row_base = (int64_t)pid * (ps_mask + 1) + (t0 & ps_mask);
-    const char* ksrc = kbase + row_base * krow_bytes;
-    const char* vsrc = vbase + row_base * vrow_bytes;
+    const char* ksrc = stage_src(kbase, (uint32_t)pid, t0, kpage_bytes, krow_bytes);
+    const char* vsrc = stage_src(vbase, (uint32_t)pid, t0, vpage_bytes, vrow_bytes);
     const uint32_t st = lds0 + slot_issue;
     if (tlim >= kPStage - 1) {
 #pragma unroll
@@ -285,21 +291,21 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     if (in_step) ++n_groups;  // the dummy group, issued in the step's slots after any stage above
   };
   // slot work of the step's group: part 0 reads the page id (in the step, so the compiler waits
-  // for that LDS read alone), parts 1..5 issue the loads
-  auto dma_part = [&](int k) __attribute__((always_inline)) {
+  // for that LDS read alone), parts 1..5 issue the loads; real_c: the group is known to be a stage
+  auto dma_part = [&](int k, auto real_c) __attribute__((always_inline)) {
     if (k == 0) {
       dma_pg = s_pg[dma_t0 >> p.log2_ps];
       return;
     }
     if (k == 1) {
-      const int64_t row_base =
-          (int64_t)__builtin_amdgcn_readfirstlane(dma_pg) * (ps_mask + 1) + (dma_t0 & ps_mask);
-      dma_k = kbase + row_base * krow_bytes;
-      dma_v = vbase + row_base * vrow_bytes;
+      const uint32_t pid = (uint32_t)__builtin_amdgcn_readfirstlane(dma_pg);
+      dma_k = stage_src(kbase, pid, dma_t0, kpage_bytes, krow_bytes);
+      dma_v = stage_src(vbase, pid, dma_t0, vpage_bytes, vrow_bytes);
     }
     const int d = k - 1;
-    const uint32_t kdst = dma_real ? dma_st + (wave + d * kPWaves) * 1024 : dma_st;
-    const uint32_t vdst = dma_real ? dma_st + kPKBytes + (wave + (d - kPKDma) * kPWaves) * 1024 : dma_st;
+    const bool real = decltype(real_c)::value || dma_real;
+    const uint32_t kdst = real ? dma_st + (wave + d * kPWaves) * 1024 : dma_st;
+    const uint32_t vdst = real ? dma_st + kPKBytes + (wave + (d - kPKDma) * kPWaves) * 1024 : dma_st;
     if (d < kPKDma) dma16_saddr(dma_k, koff[d], kdst);
     else dma16_saddr(dma_v, voff[d - kPKDma], vdst);
   };
@@ -312,6 +318,17 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     issue(in_step);
+  };
+  // the same for a step whose group is the next stage, in the steady state (3 groups after stage
+  // n + 1's)
+  auto step_sync_fast = [&]() __attribute__((always_inline)) {
+    wait_vmcnt<kPDma * (kPStages - 4)>();
+    __builtin_amdgcn_s_barrier();
+    dma_t0 = n_stages * kPStage;
+    dma_st = lds0 + slot_issue;
+    ++n_stages;
+    ++n_groups;
+    slot_issue = next_slot(slot_issue);
   };
   // ---- queries: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
   bf16x8 qf[2][12];
@@ -458,7 +475,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // slots 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
   // ring offsets of stages j - 1 (j for j = 0), j and j + 1
   uint32_t slot_prev = 0, slot_cur = 0, slot_next = next_slot(0);
-  auto step_fast = [&](auto par_c) __attribute__((always_inline)) {
+  auto step_fast = [&](auto par_c, auto real_c) __attribute__((always_inline)) {
     constexpr int par = decltype(par_c)::value;
     f32x16_t(&scs)[2] = sc[par];
     f32x16_t(&scn)[2] = sc[par ^ 1];
@@ -484,6 +501,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     };
     static_for<kSlots>([&](auto s_c) __attribute__((always_inline)) {
       constexpr int s = decltype(s_c)::value;
+      if constexpr (s == 0) mfma_wait_scores(scs[0], scs[1]);
       if constexpr (s < 16) {
         constexpr int st = s >> 1, qs = s & 1;
         mfma_pv(O[st >> 1][qs], vb[st & 3], pbr[qs][st & 1]);
@@ -493,9 +511,8 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         if constexpr (ks == 0) mfma_qk_first(scn[qs], kb[0], qf[qs][0]);
         else mfma_qk(scn[qs], kb[ks % 5], qf[qs][ks]);
       }
-      if constexpr (s == 0) mfma_wait_scores(scs[0], scs[1]);
-      if constexpr (s == 0) dma_part(0);  // the stage refill, spread over the step
-      if constexpr (s % 8 == 3) dma_part(s / 8 + 1);
+      if constexpr (s == 0) dma_part(0, real_c);  // the stage refill, spread over the step
+      if constexpr (s % 8 == 3) dma_part(s / 8 + 1, real_c);
       if constexpr (s < 10 && (s & 1) == 0) {
         constexpr int st = (s >> 1) + 3;
         vb[st & 3] = vop(vtile, st);
@@ -519,14 +536,23 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // stage 0, which holds finite data); at j = W - 1 the scores of stage W are computed, and at
   // j = W fully masked, so that step W only adds the values of stage W - 1.
   const int j_diag = (P + row0 + 1) >> 5;  // first stage that reaches past the wave's first query
+  // steps 1 .. j_steady - 1 come before the wave's diagonal and load a full stage with a staged
+  // page id (step j loads stage j + kPStages - 2): they skip every check
+  const int j_steady = W > 0 ? min(j_diag, n_defer - (kPStages - 2)) : 0;
   auto step = [&](auto par_c, int j) __attribute__((always_inline)) {
     constexpr int par = decltype(par_c)::value;
-    const bool work = j <= W && W > 0;
-    step_sync(j, work);
+    const bool steady = j > 0 && j < j_steady;
+    const bool work = steady || (j <= W && W > 0);
+    if (__builtin_expect(steady, 1)) {
+      step_sync_fast();
+      dma_real = true;
+    } else {
+      step_sync(j, work);
+    }
     if (work) {
       if (__builtin_expect(j >= j_diag, 0)) mask_scores(sc[par], j, j == W);
       if (__builtin_expect(j == 0, 0)) init_ref(sc[par]);
-      step_fast(par_c);
+      step_fast(par_c, std::false_type{});
     }
     slot_prev = slot_cur;
     slot_cur = slot_next;
