@@ -272,23 +272,21 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     ++n_groups;
     slot_issue = next_slot(slot_issue);
   };
-  auto issue = [&](bool in_step) __attribute__((always_inline)) {
-    if (in_step) {
-      if (__builtin_expect(n_stages < n_defer, 1)) {
-        dma_real = true;
-        dma_t0 = n_stages * kPStage;
-        dma_st = lds0 + slot_issue;
-        ++n_stages;
-        ++n_groups;
-        slot_issue = next_slot(slot_issue);
-        return;
-      }
-      dma_real = false;
-      dma_t0 = 0;
-      dma_st = lds_dummy;
+  // the group of a step: stage n_stages when it is a full one with a staged page id, otherwise a
+  // dummy group, preceded by the next stage issued at once if one is left (a tail stage, or any
+  // stage whose page id is not staged)
+  auto group_setup = [&]() __attribute__((always_inline)) {
+    const bool real = n_stages < n_defer;
+    dma_real = real;
+    dma_t0 = real ? n_stages * kPStage : 0;
+    dma_st = real ? lds0 + slot_issue : lds_dummy;
+    if (real) {
+      ++n_stages;
+      slot_issue = next_slot(slot_issue);
+    } else if (__builtin_expect(n_stages < nst, 0)) {
+      issue_now();
     }
-    if (n_stages < nst) issue_now();
-    if (in_step) ++n_groups;  // the dummy group, issued in the step's slots after any stage above
+    ++n_groups;
   };
   // slot work of the step's group: part 0 reads the page id (in the step, so the compiler waits
   // for that LDS read alone), parts 1..5 issue the loads; real_c: the group is known to be a stage
@@ -309,26 +307,19 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     if (d < kPKDma) dma16_saddr(dma_k, koff[d], kdst);
     else dma16_saddr(dma_v, voff[d - kPKDma], vdst);
   };
-  // stage n + 1 has landed for every wave, and every wave is done with step n - 1; the stage
-  // that step n - 1 finished with is refilled. Groups after stage n + 1's: 3 in the steady state
-  // (then at most 15 loads may stay in flight), fewer near the start and the end (then wait for
-  // all: a longer wait, never a shorter one).
-  auto step_sync = [&](int n, bool in_step) __attribute__((always_inline)) {
-    if (n_groups - 2 - n >= kPStages - 4) wait_vmcnt<kPDma * (kPStages - 4)>();
-    else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    issue(in_step);
+  // all loads of the step's group at once (a wave without work in the step, and the groups before
+  // the first step)
+  auto group_now = [&]() __attribute__((always_inline)) {
+    group_setup();
+#pragma unroll
+    for (int k = 0; k <= kPDma; ++k) dma_part(k, std::false_type{});
   };
-  // the same for a step whose group is the next stage, in the steady state (3 groups after stage
-  // n + 1's)
-  auto step_sync_fast = [&]() __attribute__((always_inline)) {
+  // stage n + 1 has landed for every wave, and every wave is done with step n - 1 (so the stage
+  // that step finished with may be refilled): every step issues exactly one group, so 3 groups
+  // follow stage n + 1's and at most 15 loads may still be in flight
+  auto step_sync = [&]() __attribute__((always_inline)) {
     wait_vmcnt<kPDma * (kPStages - 4)>();
     __builtin_amdgcn_s_barrier();
-    dma_t0 = n_stages * kPStage;
-    dma_st = lds0 + slot_issue;
-    ++n_stages;
-    ++n_groups;
-    slot_issue = next_slot(slot_issue);
   };
   // ---- queries: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
   bf16x8 qf[2][12];
@@ -346,7 +337,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int ks = 0; ks < 12; ++ks) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
 
-  while (n_stages < kPStages - 3 && n_stages < nst) issue(false);
+  for (int g = 0; g < kPStages - 3; ++g) group_now();
 
   // ---- per-lane LDS read offsets
   // K operand of k-step ks = 4m + r: chunk 8m + 2r + g32 of key c32 at k_off[r] + 128m
@@ -483,6 +474,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const u32x4(&pbr)[2][2] = pb[par ^ 1];
     const int kt = slot_next, vtile = slot_prev;
     float l_step[2], ev[2][2];  // ev: the numerators of the pair being packed (raw scores stay)
+    float l_step_max;
     auto uop = [&](auto u_c) __attribute__((always_inline)) {
       constexpr int u = decltype(u_c)::value;
       constexpr int k = u / 6, r = u % 6;
@@ -527,7 +519,11 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    if (__ballot(!(l_step[0] < kPLazyMax) || !(l_step[1] < kPLazyMax)) != 0) redo_stage(scs, pbw, l_step);
+    // any lane's sum at 2^32 or more, or infinite: one compare into a lane mask, no reduction
+    uint64_t big;
+    asm volatile("v_max_f32 %1, %2, %3\n\tv_cmp_le_f32_e64 %0, %4, %1"
+                 : "=s"(big), "=&v"(l_step_max) : "v"(l_step[0]), "v"(l_step[1]), "v"(kPLazyMax));
+    if (big != 0) redo_stage(scs, pbw, l_step);
     l_run[0] += l_step[0];
     l_run[1] += l_step[1];
   };
@@ -536,23 +532,16 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // stage 0, which holds finite data); at j = W - 1 the scores of stage W are computed, and at
   // j = W fully masked, so that step W only adds the values of stage W - 1.
   const int j_diag = (P + row0 + 1) >> 5;  // first stage that reaches past the wave's first query
-  // steps 1 .. j_steady - 1 come before the wave's diagonal and load a full stage with a staged
-  // page id (step j loads stage j + kPStages - 2): they skip every check
-  const int j_steady = W > 0 ? min(j_diag, n_defer - (kPStages - 2)) : 0;
   auto step = [&](auto par_c, int j) __attribute__((always_inline)) {
     constexpr int par = decltype(par_c)::value;
-    const bool steady = j > 0 && j < j_steady;
-    const bool work = steady || (j <= W && W > 0);
-    if (__builtin_expect(steady, 1)) {
-      step_sync_fast();
-      dma_real = true;
-    } else {
-      step_sync(j, work);
-    }
-    if (work) {
+    step_sync();
+    if (__builtin_expect(j <= W && W > 0, 1)) {
+      group_setup();
       if (__builtin_expect(j >= j_diag, 0)) mask_scores(sc[par], j, j == W);
       if (__builtin_expect(j == 0, 0)) init_ref(sc[par]);
       step_fast(par_c, std::false_type{});
+    } else {
+      group_now();
     }
     slot_prev = slot_cur;
     slot_cur = slot_next;
@@ -563,7 +552,8 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // without rows has W = 0 and only takes the barriers: its "step 0" work is skipped below.
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
-  step_sync(-1, false);
+  step_sync();
+  group_now();
   if (W > 0) {
     qk_plain(sc[0], 0);
     vb[0] = vop(0, 0);
