@@ -35,11 +35,24 @@ __device__ __forceinline__ void wait_vmcnt() {
 // lds_base + 16*i. Issued as inline asm so that the compiler's wait-count
 // pass does not serialise later LDS reads of other stages behind it: every
 // read of a staged tile is preceded by wait_vmcnt + a workgroup barrier.
+// The compiler's hazard recognizer does not look inside inline asm, so the
+// wait states it would add are written here: an LDS DMA reads M0 one wait
+// state after a scalar write of M0 (the compiler writes M0 just before the
+// asm statement).
 __device__ __forceinline__ void dma16_saddr(const char* base, uint32_t voff, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
 }
 __device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
+}
+// A 64-bit scalar base from a uniform vector value, for a DMA's address. A vector-ALU write of an
+// SGPR needs 5 wait states before a memory instruction reads it; readfirstlane and the nops are
+// volatile asm, so they stay in order with the DMA asm statements that follow.
+__device__ __forceinline__ const char* uniform_ptr(uint32_t lo, uint32_t hi) {
+  uint32_t slo, shi;
+  asm volatile("v_readfirstlane_b32 %0, %2\n\tv_readfirstlane_b32 %1, %3\n\ts_nop 4"
+               : "=s"(slo), "=s"(shi) : "v"(lo), "v"(hi));
+  return reinterpret_cast<const char*>(((uint64_t)shi << 32) | slo);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {

@@ -42,11 +42,11 @@ constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
 constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
 constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
 constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
-constexpr int kPStages = 7;
+constexpr int kPStages = 6;  // ring stages; the loop over the steps is unrolled by this
 constexpr int kPKDma = kPKBytes / 1024 / kPWaves;  // 3 wave-wide DMA loads per wave
 constexpr int kPVDma = kPVBytes / 1024 / kPWaves;  // 2
 constexpr int kPDma = kPKDma + kPVDma;             // 5
-constexpr int kPMaxPages = 1024;  // page ids of a CTA's keys staged in LDS (else read per stage)
+constexpr int kPMaxGroups = 1024;  // stage sources of a CTA staged in LDS (else computed per stage)
 
 // ---- the softmax of one stage as a list of micro-operations, spread over the 40 MFMA slots of a
 // pipelined step in proportion to their cost (~4-cycle units; next to running MFMAs a vector
@@ -126,9 +126,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kPStages * kPStageBytes];
-  __shared__ int s_pg[kPMaxPages];
-  __shared__ __attribute__((aligned(1024))) char s_dummy[1024];  // destination of dummy DMA groups
+  // the ring, then one stage-sized area that dummy DMA groups load into
+  __shared__ __attribute__((aligned(1024))) char smem[(kPStages + 1) * kPStageBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t s_src[kPMaxGroups + 1][4];  // K and V source of stage g
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -186,7 +186,6 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   const int c32 = lane & 31;
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
-  const uint32_t lds_dummy = (uint32_t)(uintptr_t)(MLA_LDS char*)s_dummy;
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * kPKRowBytes;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * kPVRowBytes;
   const int krow_bytes = (int)(p.k_row_stride * 2), vrow_bytes = (int)(p.v_row_stride * 2);
@@ -198,12 +197,17 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     return base + ((uint64_t)pid * page_bytes + (uint32_t)((t0 & ps_mask) * row_bytes));
   };
 
-  // ---- page ids of the CTA's keys
-  const int npages = __builtin_amdgcn_readfirstlane((nkeys + ps_mask) >> p.log2_ps);
-  const bool staged = npages <= kPMaxPages;
-  // (unstaged, s_pg[0] still holds the first page: the source of dummy DMA groups)
-  for (int i = threadIdx.x; i < (staged ? npages : 1); i += 256)
-    s_pg[i] = min(max(p.page_table[(int64_t)b * p.pt_stride + i], 0), p.num_pages - 1);
+  // ---- source addresses of the CTA's full stages (s_src[n_defer]: the first stage's, the source
+  // of dummy groups); a CTA with more stages than that computes each stage's source when it loads it
+  const bool staged = nst <= kPMaxGroups;
+  const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
+  for (int g = threadIdx.x; g <= n_defer; g += 256) {
+    const int t0 = g < n_defer ? g * kPStage : 0;
+    const uint32_t pid = (uint32_t)min(max(p.page_table[(int64_t)b * p.pt_stride + (t0 >> p.log2_ps)], 0), p.num_pages - 1);
+    const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
+    const uint64_t va = (uint64_t)stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
+    *reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g) = u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
+  }
   __syncthreads();
 
   // ---- DMA of stage n (32 tokens of one page: page_size >= 64); rows past the last key load the
@@ -220,103 +224,82 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const int s = (wave + k * kPWaves) * 64 + lane, t = s >> 4;
     voff[k] = (uint32_t)(t * vrow_bytes + vswz(s & 15, t) * 16);
   }
-  // DMA groups (5 loads per wave) are issued in order; real stages in stage order, a dummy group
-  // never ahead of a real stage. A pipelined step issues exactly one group, one load at a time in
-  // its slots: the next stage when it is a full one with a staged page id, otherwise a dummy group
-  // (page 0 of the request again, into a 1 KB scratch area of LDS), so that the slots carry no
-  // branches; tail stages (and unstaged page ids) are issued at once, ahead of that dummy.
+  // DMA groups (5 loads per wave) are issued in order, real stages in stage order, stage n into
+  // ring slot n % kPStages. Every step issues exactly one group, one load at a time in its slots:
+  // the next stage when it is a full one with a staged source, otherwise a dummy group (the first
+  // stage again, into the dummy area), so that the slots carry no branches; a tail stage (and every
+  // stage of a CTA without staged sources) is issued at once, ahead of that dummy.
   int n_stages = 0, n_groups = 0;
-  uint32_t slot_issue = 0;  // ring offset of stage n_stages
-  const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
-  int dma_t0 = 0, dma_pg = 0;  // token offset and page id of the step's group
-  uint32_t dma_st = 0;        // its LDS destination (stage slot or scratch)
-  bool dma_real = false;
-  const char* dma_k = kbase;
-  const char* dma_v = vbase;
-  auto next_slot = [&](uint32_t o) __attribute__((always_inline)) {
-    return o + kPStageBytes == kPStages * kPStageBytes ? 0u : o + kPStageBytes;
-  };
+  const uint32_t lds_dummy = lds0 + kPStages * kPStageBytes;
+  int dma_idx = 0;       // s_src entry of the step's group
+  uint32_t dma_m0w = 0;  // its LDS destination, this wave's first 1 KB
   auto issue_now = [&]() __attribute__((always_inline)) {  // stage n_stages < nst, all loads now
     const int t0 = n_stages * kPStage;
     const int tlim = L - 1 - t0;
-    const int pid = staged ? __builtin_amdgcn_readfirstlane(s_pg[t0 >> p.log2_ps])
-                           : min(max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0),
-                                 p.num_pages - 1);
-    const char* ksrc = stage_src(kbase, (uint32_t)pid, t0, kpage_bytes, krow_bytes);
-    const char* vsrc = stage_src(vbase, (uint32_t)pid, t0, vpage_bytes, vrow_bytes);
-    const uint32_t st = lds0 + slot_issue;
-    if (tlim >= kPStage - 1) {
+    const uint32_t pid = (uint32_t)min(
+        max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0), p.num_pages - 1);
+    const char* ksrc = stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
+    const char* vsrc = stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
+    const uint32_t st = lds0 + (uint32_t)(n_stages % kPStages) * kPStageBytes;
+    // rows past the last key reload the last key (the lane index from a volatile asm, so that these
+    // offsets are computed here and not kept in registers across the loop)
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
-      for (int k = 0; k < kPKDma; ++k) dma16_saddr(ksrc, koff[k], st + (wave + k * kPWaves) * 1024);
+    for (int k = 0; k < kPKDma; ++k) {
+      const int s = (wave + k * kPWaves) * 64 + ln, t = s / 24;
+      const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes + kswz(s - 24 * t, t) * 16);
+      dma16_saddr(ksrc, o, st + (wave + k * kPWaves) * 1024);
+    }
 #pragma unroll
-      for (int k = 0; k < kPVDma; ++k) dma16_saddr(vsrc, voff[k], st + kPKBytes + (wave + k * kPWaves) * 1024);
-    } else {  // the request's last stage: rows past the last key reload the last key
-      // lane index from a volatile asm, so that these offsets are computed here and not kept in
-      // registers across the loop
-      int ln;
-      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-#pragma unroll
-      for (int k = 0; k < kPKDma; ++k) {
-        const int s = (wave + k * kPWaves) * 64 + ln, t = s / 24;
-        const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes + kswz(s - 24 * t, t) * 16);
-        dma16_saddr(ksrc, o, st + (wave + k * kPWaves) * 1024);
-      }
-#pragma unroll
-      for (int k = 0; k < kPVDma; ++k) {
-        const int s = (wave + k * kPWaves) * 64 + ln, t = s >> 4;
-        const uint32_t o = (uint32_t)(min(t, tlim) * vrow_bytes + vswz(s & 15, t) * 16);
-        dma16_saddr(vsrc, o, st + kPKBytes + (wave + k * kPWaves) * 1024);
-      }
+    for (int k = 0; k < kPVDma; ++k) {
+      const int s = (wave + k * kPWaves) * 64 + ln, t = s >> 4;
+      const uint32_t o = (uint32_t)(min(t, tlim) * vrow_bytes + vswz(s & 15, t) * 16);
+      dma16_saddr(vsrc, o, st + kPKBytes + (wave + k * kPWaves) * 1024);
     }
     ++n_stages;
     ++n_groups;
-    slot_issue = next_slot(slot_issue);
   };
-  // the group of a step: stage n_stages when it is a full one with a staged page id, otherwise a
-  // dummy group, preceded by the next stage issued at once if one is left (a tail stage, or any
-  // stage whose page id is not staged)
-  auto group_setup = [&]() __attribute__((always_inline)) {
-    const bool real = n_stages < n_defer;
-    dma_real = real;
-    dma_t0 = real ? n_stages * kPStage : 0;
-    dma_st = real ? lds0 + slot_issue : lds_dummy;
-    if (real) {
-      ++n_stages;
-      slot_issue = next_slot(slot_issue);
-    } else if (__builtin_expect(n_stages < nst, 0)) {
-      issue_now();
-    }
+  // the group of a step; slot_c: the ring slot of the group when it is a real one (step j loads
+  // stage j + kPStages - 2, the unrolled loop knows j % kPStages), or -1 to compute it
+  auto group_setup = [&](auto slot_c) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot_c)::value;
+    const bool real = n_groups < n_defer;
+    dma_idx = real ? n_groups : n_defer;
+    const uint32_t slot = SL >= 0 ? (uint32_t)SL * kPStageBytes : (uint32_t)(n_groups % kPStages) * kPStageBytes;
+    dma_m0w = (real ? lds0 + slot : lds_dummy) + wave * 1024;
+    if (real) ++n_stages;
+    else if (__builtin_expect(n_stages < nst, 0)) issue_now();
     ++n_groups;
   };
-  // slot work of the step's group: part 0 reads the page id (in the step, so the compiler waits
-  // for that LDS read alone), parts 1..5 issue the loads; real_c: the group is known to be a stage
-  auto dma_part = [&](int k, auto real_c) __attribute__((always_inline)) {
+  // slot work of the step's group: part 0 reads its sources (in the step, so the compiler waits
+  // for that LDS read alone), parts 1..5 issue the loads
+  u32x4 dma_e;
+  const char* dma_k = kbase;
+  const char* dma_v = vbase;
+  auto dma_part = [&](int k) __attribute__((always_inline)) {
     if (k == 0) {
-      dma_pg = s_pg[dma_t0 >> p.log2_ps];
+      dma_e = *reinterpret_cast<const MLA_LDS u32x4*>((const MLA_LDS char*)s_src + 16 * dma_idx);
       return;
     }
     if (k == 1) {
-      const uint32_t pid = (uint32_t)__builtin_amdgcn_readfirstlane(dma_pg);
-      dma_k = stage_src(kbase, pid, dma_t0, kpage_bytes, krow_bytes);
-      dma_v = stage_src(vbase, pid, dma_t0, vpage_bytes, vrow_bytes);
+      dma_k = uniform_ptr(dma_e[0], dma_e[1]);
+      dma_v = uniform_ptr(dma_e[2], dma_e[3]);
     }
     const int d = k - 1;
-    const bool real = decltype(real_c)::value || dma_real;
-    const uint32_t kdst = real ? dma_st + (wave + d * kPWaves) * 1024 : dma_st;
-    const uint32_t vdst = real ? dma_st + kPKBytes + (wave + (d - kPKDma) * kPWaves) * 1024 : dma_st;
-    if (d < kPKDma) dma16_saddr(dma_k, koff[d], kdst);
-    else dma16_saddr(dma_v, voff[d - kPKDma], vdst);
+    if (d < kPKDma) dma16_saddr(dma_k, koff[d], dma_m0w + d * kPWaves * 1024);
+    else dma16_saddr(dma_v, voff[d - kPKDma], dma_m0w + kPKBytes + (d - kPKDma) * kPWaves * 1024);
   };
   // all loads of the step's group at once (a wave without work in the step, and the groups before
   // the first step)
-  auto group_now = [&]() __attribute__((always_inline)) {
-    group_setup();
+  auto group_now = [&](auto slot_c) __attribute__((always_inline)) {
+    group_setup(slot_c);
 #pragma unroll
-    for (int k = 0; k <= kPDma; ++k) dma_part(k, std::false_type{});
+    for (int k = 0; k <= kPDma; ++k) dma_part(k);
   };
   // stage n + 1 has landed for every wave, and every wave is done with step n - 1 (so the stage
-  // that step finished with may be refilled): every step issues exactly one group, so 3 groups
-  // follow stage n + 1's and at most 15 loads may still be in flight
+  // that step finished with may be refilled): every step issues exactly one group, so
+  // kPStages - 4 groups follow stage n + 1's and at most 5 (kPStages - 4) loads may still be in flight
   auto step_sync = [&]() __attribute__((always_inline)) {
     wait_vmcnt<kPDma * (kPStages - 4)>();
     __builtin_amdgcn_s_barrier();
@@ -337,7 +320,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int ks = 0; ks < 12; ++ks) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
 
-  for (int g = 0; g < kPStages - 3; ++g) group_now();
+  for (int g = 0; g < kPStages - 3; ++g) group_now(ic<-1>{});
 
   // ---- per-lane LDS read offsets
   // K operand of k-step ks = 4m + r: chunk 8m + 2r + g32 of key c32 at k_off[r] + 128m
@@ -465,8 +448,13 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // by scheduling barriers. V^T operands 0..2 are read by the step before (slots 36..38), 3..7 in
   // slots 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
   // ring offsets of stages j - 1 (j for j = 0), j and j + 1
-  uint32_t slot_prev = 0, slot_cur = 0, slot_next = next_slot(0);
-  auto step_fast = [&](auto par_c, auto real_c) __attribute__((always_inline)) {
+  // step j = j0 + U with j0 a multiple of kPStages: ring slots (U - 1, U, U + 1) % kPStages hold
+  // stages j - 1, j and j + 1, and the step loads stage j + kPStages - 2 into slot (U - 2) % kPStages
+  auto step_fast = [&](auto par_c, auto u_c) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_c)::value;
+    constexpr int slot_prev = (U + kPStages - 1) % kPStages * kPStageBytes;
+    constexpr int slot_cur = U * kPStageBytes;
+    constexpr int slot_next = (U + 1) % kPStages * kPStageBytes;
     constexpr int par = decltype(par_c)::value;
     f32x16_t(&scs)[2] = sc[par];
     f32x16_t(&scn)[2] = sc[par ^ 1];
@@ -503,8 +491,8 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         if constexpr (ks == 0) mfma_qk_first(scn[qs], kb[0], qf[qs][0]);
         else mfma_qk(scn[qs], kb[ks % 5], qf[qs][ks]);
       }
-      if constexpr (s == 0) dma_part(0, real_c);  // the stage refill, spread over the step
-      if constexpr (s % 8 == 3) dma_part(s / 8 + 1, real_c);
+      if constexpr (s == 0) dma_part(0);  // the stage refill, spread over the step
+      if constexpr (s % 8 == 3) dma_part(s / 8 + 1);
       if constexpr (s < 10 && (s & 1) == 0) {
         constexpr int st = (s >> 1) + 3;
         vb[st & 3] = vop(vtile, st);
@@ -532,38 +520,36 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // stage 0, which holds finite data); at j = W - 1 the scores of stage W are computed, and at
   // j = W fully masked, so that step W only adds the values of stage W - 1.
   const int j_diag = (P + row0 + 1) >> 5;  // first stage that reaches past the wave's first query
-  auto step = [&](auto par_c, int j) __attribute__((always_inline)) {
-    constexpr int par = decltype(par_c)::value;
+  auto step = [&](auto u_c, int j) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_c)::value;
+    constexpr int par = U & 1;
+    using slot_c = ic<(U + kPStages - 2) % kPStages>;
     step_sync();
     if (__builtin_expect(j <= W && W > 0, 1)) {
-      group_setup();
+      group_setup(slot_c{});
       if (__builtin_expect(j >= j_diag, 0)) mask_scores(sc[par], j, j == W);
       if (__builtin_expect(j == 0, 0)) init_ref(sc[par]);
-      step_fast(par_c, std::false_type{});
+      step_fast(ic<par>{}, u_c);
     } else {
-      group_now();
+      group_now(slot_c{});
     }
-    slot_prev = slot_cur;
-    slot_cur = slot_next;
-    slot_next = next_slot(slot_next);
   };
 
-  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier). A wave
-  // without rows has W = 0 and only takes the barriers: its "step 0" work is skipped below.
+  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier), rounded up to
+  // whole rounds of the ring (the steps past nst only load dummy groups). A wave without rows has
+  // W = 0 and only takes the barriers and loads its groups.
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
   step_sync();
-  group_now();
+  group_now(ic<-1>{});
   if (W > 0) {
     qk_plain(sc[0], 0);
     vb[0] = vop(0, 0);
     vb[1] = vop(0, 1);
     vb[2] = vop(0, 2);
   }
-  for (int j = 0; j <= nst; j += 2) {
-    step(ic<0>{}, j);
-    if (j + 1 <= nst) step(ic<1>{}, j + 1);
-  }
+  for (int j0 = 0; j0 <= nst; j0 += kPStages)
+    static_for<kPStages>([&](auto u_c) __attribute__((always_inline)) { step(u_c, j0 + decltype(u_c)::value); });
 
   // ---- finalise: lane holds query column c32 and dims 32db + 8(i/4) + 4*g32 + i%4
 #pragma unroll
