@@ -108,7 +108,8 @@ int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
  *   page_table [batch, >= ceil(seq_len/page_size)] int32, row stride pt_stride
  *   seq_lens [batch] int32 (device_len, includes the token being decoded)
  *   plan     device copy of mla_decode_plan's cta_ranges followed by req_info
- *   ws_o     [ws_slots, heads, 512] fp32, ws_lse [ws_slots, heads] fp32
+ *   ws_o     [ws_slots, heads, 512] bf16 (normalised partial outputs),
+ *            ws_lse [ws_slots, heads] fp32
  *   out      [batch, heads, 512] strides (out_stride_b, out_stride_h)
  *   lse      [batch, heads] fp32 (row stride lse_stride_b) or NULL
  * heads is 16, 32, 48 or 64 (one wave per 16 heads); page_size a power of
@@ -119,14 +120,14 @@ int mla_decode_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h, const
                     int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
                     const int32_t *page_table, int64_t pt_stride, const int32_t *seq_lens,
                     int32_t batch, int32_t heads, float scale, const int32_t *plan,
-                    int32_t num_ctas, float *ws_o, float *ws_lse, int32_t ws_slots, void *out,
+                    int32_t num_ctas, void *ws_o, float *ws_lse, int32_t ws_slots, void *out,
                     int64_t out_stride_b, int64_t out_stride_h, float *lse, int64_t lse_stride_b,
                     void *stream);
 
 /*
  * The split step of mla_decode_bf16 alone (same arguments): requests covered
  * by one piece get their final bf16 output and LSE, split requests leave
- * normalised fp32 partials in ws_o / ws_lse for mla_decode_merge_f32 with
+ * normalised partials (bf16 outputs, fp32 LSE) in ws_o / ws_lse for mla_decode_merge_f32 with
  * single_piece_final = 1. No counterpart in the reference (its decode is one
  * opaque library call); it is the unit a sequence-sharded decode distributes.
  */
@@ -134,12 +135,12 @@ int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                           const void *kv_pool, int64_t kv_row_stride, int32_t num_pages,
                           int32_t page_size, const int32_t *page_table, int64_t pt_stride,
                           const int32_t *seq_lens, int32_t batch, int32_t heads, float scale,
-                          const int32_t *plan, int32_t num_ctas, float *ws_o, float *ws_lse,
+                          const int32_t *plan, int32_t num_ctas, void *ws_o, float *ws_lse,
                           int32_t ws_slots, void *out, int64_t out_stride_b,
                           int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
 
 /*
- * fp32 log-sum-exp merge of split-KV partials (the merge step of
+ * fp32 log-sum-exp merge of split-KV partials (bf16 ws_o, fp32 ws_lse; the merge step of
  * mla_decode_bf16). For request b with n = req_info[3b+1] pieces in slots
  * s = req_info[3b+2] .. +n-1:
  *   lse = ln sum_i exp(ws_lse[s_i]);  out = sum_i exp(ws_lse[s_i] - lse) * ws_o[s_i]
@@ -147,7 +148,7 @@ int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
  * with n == 1 are skipped (the split step already wrote them); otherwise
  * their one slot is converted like any other.
  */
-int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slots,
+int mla_decode_merge_f32(const void *ws_o, const float *ws_lse, int32_t ws_slots,
                          const int32_t *req_info, int32_t batch, int32_t heads,
                          int32_t single_piece_final, void *out, int64_t out_stride_b,
                          int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);

@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 3; }
+int mla_abi_version(void) { return 4; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -244,7 +244,7 @@ static int check_out(const void* out, int64_t sb, int64_t sh, const float* lse, 
 static int decode_params(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          const void* kv_pool, int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
                          const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens, int32_t batch,
-                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, float* ws_o,
+                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, void* ws_o,
                          float* ws_lse, int32_t ws_slots, void* out, int64_t out_stride_b, int64_t out_stride_h,
                          float* lse, int64_t lse_stride_b, mla::DecodeParams* p) {
   if (heads != 16 && heads != 32 && heads != 48 && heads != 64)
@@ -281,7 +281,7 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
   p->scale_log2 = scale * 1.4426950408889634f;
   p->plan = plan;
   p->num_ctas = num_ctas;
-  p->ws_o = ws_o;
+  p->ws_o = static_cast<__bf16*>(ws_o);
   p->ws_lse = ws_lse;
   p->ws_slots = ws_slots;
   p->out = static_cast<__bf16*>(out);
@@ -292,12 +292,12 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
   return MLA_OK;
 }
 
-static mla::MergeParams merge_params(const float* ws_o, const float* ws_lse, int32_t ws_slots,
+static mla::MergeParams merge_params(const void* ws_o, const float* ws_lse, int32_t ws_slots,
                                      const int32_t* req_info, int32_t batch, int32_t heads, int32_t skip_single,
                                      void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                                      int64_t lse_stride_b) {
   mla::MergeParams m;
-  m.ws_o = ws_o;
+  m.ws_o = static_cast<const __bf16*>(ws_o);
   m.ws_lse = ws_lse;
   m.ws_slots = ws_slots;
   m.req_info = req_info;
@@ -315,7 +315,7 @@ static mla::MergeParams merge_params(const float* ws_o, const float* ws_lse, int
 int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                           int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                           int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                          const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                          const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
                           void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                           int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_split_bf16";
@@ -332,7 +332,7 @@ int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                     int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                     int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                    const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
                     void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
                     void* stream) {
   const char* who = "mla_decode_bf16";
@@ -350,7 +350,7 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
   return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch");
 }
 
-int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
+int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
                          int32_t batch, int32_t heads, int32_t single_piece_final, void* out, int64_t out_stride_b,
                          int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_merge_f32";

@@ -48,7 +48,7 @@ struct DecodeParams {
   float scale_log2;  // softmax scale * log2(e)
   const int32_t* plan;  // [num_ctas * 4] ranges, then [batch * 3] request info
   int32_t num_ctas;
-  float* ws_o;    // [ws_slots, H, 512]
+  __bf16* ws_o;   // [ws_slots, H, 512] normalised partial outputs
   float* ws_lse;  // [ws_slots, H]
   int32_t ws_slots;
   __bf16* out;  // [B, H, 512]
@@ -58,7 +58,7 @@ struct DecodeParams {
 };
 
 struct MergeParams {
-  const float* ws_o;
+  const __bf16* ws_o;
   const float* ws_lse;
   int32_t ws_slots;
   const int32_t* req_info;  // [batch * 3]

@@ -281,9 +281,14 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     } else {
       const int slot = slot_base + (w - first_cta);
       if (slot >= 0 && slot < p.ws_slots) {
-        float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 4 * g;
+        __bf16* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 32; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[db] * inv;
+        for (int db = 0; db < 32; ++db) {
+          u32x2 v;
+          v[0] = pack_bf16x2(O[db][0] * inv, O[db][1] * inv);
+          v[1] = pack_bf16x2(O[db][2] * inv, O[db][3] * inv);
+          *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+        }
         if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
       }
     }
@@ -333,9 +338,15 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
           const int s = base + i0 + u0 + u;
           a[u] = bq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
           if (u0 + u < cnt && s >= 0 && s < p.ws_slots) {
-            const f32x4* src = reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
-            a[u] = src[0];
-            bq[u] = src[1];
+            const u32x4 w = *reinterpret_cast<const u32x4*>(p.ws_o +
+                                                            ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              a[u][2 * j] = __uint_as_float(w[j] << 16);
+              a[u][2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+              bq[u][2 * j] = __uint_as_float(w[2 + j] << 16);
+              bq[u][2 * j + 1] = __uint_as_float(w[2 + j] & 0xffff0000u);
+            }
           }
         }
 #pragma unroll

@@ -450,9 +450,14 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
         } else {
           const int slot = __builtin_amdgcn_readfirstlane(s_slot0[comp.r]) + w;
           if (slot >= 0 && slot < p.ws_slots) {
-            float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * th + 4 * g;
+            __bf16* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * th + 4 * g;
 #pragma unroll
-            for (int db = 0; db < 16; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[hb][db] * inv;
+            for (int db = 0; db < 16; ++db) {
+              u32x2 v;
+              v[0] = pack_bf16x2(O[hb][db][0] * inv, O[hb][db][1] * inv);
+              v[1] = pack_bf16x2(O[hb][db][2] * inv, O[hb][db][3] * inv);
+              *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+            }
             stores += 16;
             if (th == 0) {
               if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;

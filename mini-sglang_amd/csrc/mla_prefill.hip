@@ -197,6 +197,17 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     return base + ((uint64_t)pid * page_bytes + (uint32_t)((t0 & ps_mask) * row_bytes));
   };
 
+  // ---- queries, loaded first so that their latency overlaps the page-table reads below:
+  // qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
+  bf16x8 qf[2][12];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int row = row0 + 32 * qs + c32;
+    const bool ok = row < E;
+    const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)h * p.q_stride_h + 8 * g32;
+#pragma unroll
+    for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = ok ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ks) : bf16x8{};
+  }
   // ---- source addresses of the CTA's full stages (s_src[n_defer]: the first stage's, the source
   // of dummy groups); a CTA with more stages than that computes each stage's source when it loads it
   const bool staged = nst <= kPMaxGroups;
@@ -238,8 +249,12 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const int tlim = L - 1 - t0;
     const uint32_t pid = (uint32_t)min(
         max(sload_i32(p.page_table + (int64_t)b * p.pt_stride + (t0 >> p.log2_ps)), 0), p.num_pages - 1);
-    const char* ksrc = stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
-    const char* vsrc = stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
+    // (the sources through readfirstlane: under register pressure the compiler may keep these
+    // uniform values in vector registers, which the DMA's scalar base operand cannot take)
+    const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
+    const uint64_t va = (uint64_t)stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
+    const char* ksrc = uniform_ptr((uint32_t)ka, (uint32_t)(ka >> 32));
+    const char* vsrc = uniform_ptr((uint32_t)va, (uint32_t)(va >> 32));
     const uint32_t st = lds0 + (uint32_t)(n_stages % kPStages) * kPStageBytes;
     // rows past the last key reload the last key (the lane index from a volatile asm, so that these
     // offsets are computed here and not kept in registers across the loop)
@@ -304,16 +319,6 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     wait_vmcnt<kPDma * (kPStages - 4)>();
     __builtin_amdgcn_s_barrier();
   };
-  // ---- queries: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
-  bf16x8 qf[2][12];
-#pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int row = row0 + 32 * qs + c32;
-    const bool ok = row < E;
-    const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)h * p.q_stride_h + 8 * g32;
-#pragma unroll
-    for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = ok ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ks) : bf16x8{};
-  }
   // the queries stay in accumulation registers for the whole kernel (the score MFMAs read them there)
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs)

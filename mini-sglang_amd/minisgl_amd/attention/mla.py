@@ -85,7 +85,7 @@ class MLAAttnBackend(BaseAttnBackend):
             return
         assert self.capture is None, "captured graphs hold the workspace: it is sized once in init_capture_graph"
         assert not torch.cuda.is_current_stream_capturing(), "workspace must be sized before capture"
-        self.ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.float32, device=self.device)
+        self.ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.bfloat16, device=self.device)
         self.ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
 
     # ------------------------------------------------------------------ forward

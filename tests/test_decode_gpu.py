@@ -29,7 +29,7 @@ def run_decode(q, kv, pt, seq_lens, lens, ps, num_ctas, scale=R.DEFAULT_SCALE):
     B, H, _ = q.shape
     plan_np, slots = lib.decode_plan(lens, ps, num_ctas)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=DEV)
+    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.bfloat16, device=DEV)
     ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=DEV)
     out = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
     lse = torch.full((B, H), float("nan"), dtype=torch.float32, device=DEV)
@@ -116,7 +116,7 @@ def test_decode_64_heads_page_sizes(ps, num_ctas):
 def test_merge_kernel_standalone():
     gen = torch.Generator().manual_seed(5)
     H, S = 16, 11
-    o_parts = torch.randn((S, H, 512), generator=gen)
+    o_parts = torch.randn((S, H, 512), generator=gen).to(torch.bfloat16)  # partials are bf16
     lse_parts = torch.randn((S, H), generator=gen) * 3
     lse_parts[4] = float("-inf")  # an empty piece
     req_info = torch.tensor([[0, 3, 0], [0, 1, 3], [0, 0, 0], [0, 7, 4]], dtype=torch.int32)
@@ -125,7 +125,7 @@ def test_merge_kernel_standalone():
     lib.mla_decode_merge(o_parts.to(DEV), lse_parts.to(DEV), req_info.flatten().to(DEV), out, lse)
     torch.cuda.synchronize()
     for b, (_, n, base) in enumerate(req_info.tolist()):
-        o_ref, l_ref = R.mla_merge(o_parts[base : base + n], lse_parts[base : base + n])
+        o_ref, l_ref = R.mla_merge(o_parts[base : base + n].float(), lse_parts[base : base + n])
         torch.testing.assert_close(out[b].float().cpu(), o_ref, **O_TOL)
         torch.testing.assert_close(lse[b].cpu(), l_ref, **LSE_TOL)
 
@@ -171,7 +171,7 @@ def test_split_then_merge_equals_one_call():
     q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
     plan_np, slots = lib.decode_plan(case.lens, 64, 32)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), 64, 512), dtype=torch.float32, device=DEV)
+    ws_o = torch.empty((max(slots, 1), 64, 512), dtype=torch.bfloat16, device=DEV)
     ws_lse = torch.empty((max(slots, 1), 64), dtype=torch.float32, device=DEV)
     outs = []
     for two_step in (False, True):
