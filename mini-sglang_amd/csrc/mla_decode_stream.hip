@@ -81,6 +81,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     const int s = (wave + k * kSWaves) * 64 + lane;
     const int t = (s * 7282) >> 19;  // s / 72 for s < 2304
     dma_voff[k] = t * row_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4);
+    // kept in an accumulation register (one move per use): otherwise the compiler recomputes the
+    // offset (about ten vector instructions) at every tile for want of a free vector register
+    asm volatile("" : "=a"(dma_voff[k]) : "0"(dma_voff[k]));
   }
 
   // ---- stage the range: request bounds, then one page id per 32-token tile
