@@ -13,6 +13,7 @@ class MLAConfig:
     qk_rope_head_dim: int = 64
     qk_nope_head_dim: int = 128
     v_head_dim: int = 128
+    softmax_mscale: float = 1.0  # YaRN attention factor; the scale is multiplied by its square
 
     @property
     def kv_dim(self) -> int:
@@ -26,4 +27,4 @@ class MLAConfig:
 
     @property
     def softmax_scale(self) -> float:
-        return self.qk_head_dim**-0.5
+        return self.softmax_mscale**2 * self.qk_head_dim**-0.5

@@ -97,6 +97,10 @@ class MLAKVCache(BaseKVCachePool):
     def page_size(self) -> int:
         return self._page_size
 
+    @property
+    def has_prefill_pages(self) -> bool:
+        return self._k_heads is not None
+
     def latent_cache(self, index: int) -> torch.Tensor:
         return self._latent[index]
 

@@ -1,0 +1,228 @@
+"""DeepSeek-V3 / Kimi-K2 multi-head latent attention layer: the caller of the MLA backend.
+
+The reference's only attention caller is the MHA ``AttentionLayer``
+(python/minisgl/layers/attention.py:17-57): split qkv, norm, RoPE, then
+``ctx.attn_backend.forward(q, k, v, layer_id, ctx.batch)``. This layer plays the same role for
+MLA, with the same context protocol (``get_global_ctx()``: the active batch, the backend, the
+KV pool):
+
+* queries: ``q = W_qb . rmsnorm(W_qa . x)`` -> ``[T, H, 192]`` = 128 "nope" + 64 rope dims;
+* keys/values: ``[c | k_pe] = W_kva . x`` (``c`` the 512-wide latent, normed; ``k_pe`` the 64
+  rope dims shared by all heads); RoPE on ``q_pe`` and ``k_pe`` at ``batch.positions``;
+* ``W_kvb`` decompresses the latent per head: ``k_nope = W_UK c`` and ``v = W_UV c``
+  (``W_kvb`` rows are ``[H, 128 + 128]`` over the 512 latent columns);
+* decode (absorbed): ``q_lat = q_nope W_UK`` -> ``[T, H, 512]``, the backend attends
+  ``[q_lat | q_pe]`` over the latent rows ``[c | k_pe]`` and returns ``o_lat [T, H, 512]``,
+  then ``o = o_lat W_UV^T`` -> ``[T, H, 128]``;
+* prefill (decompressed): ``k = [k_nope | k_pe]`` ``[T, H, 192]`` and ``v [T, H, 128]``, the
+  backend attends ``q`` causally over the per-head pages;
+* ``out = W_o . o``.
+
+Every new token's latent row is stored (decode reads it); when the pool also holds per-head
+pages, every new token's decompressed K/V is stored there too, so a later prefill chunk (or a
+new request reusing this prefix) finds its whole prefix decompressed.
+
+RoPE: the cos/sin cache of python/minisgl/layers/rotary.py:22-31 (``[max_position, d]``, the
+``d/2`` cosines then the ``d/2`` sines) with its YaRN frequency blend (rotary.py:92-111);
+DeepSeek/Kimi checkpoints rotate interleaved pairs ``(2i, 2i+1)`` (``rope_interleaved``), the
+reference's MHA models rotate halves ``(i, i + d/2)``. YaRN also scales the softmax by
+``mscale^2`` with ``mscale = 0.1 * mscale_all_dim * ln(factor) + 1`` (the YaRN paper's
+attention factor as DeepSeek-V3 applies it), carried by ``MLAConfig.softmax_mscale`` so that
+the backend's scale agrees.
+
+The GEMMs are plain library GEMMs (torch.matmul / bmm on hipBLASLt); the attention is the HIP
+library. Tensor-parallel sharding is out of scope (one GPU): ``num_heads`` is this rank's.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Tuple
+
+import torch
+
+from ..config import MLAConfig
+from ..core import get_global_ctx
+
+
+@dataclass(frozen=True)
+class MLALayerConfig:
+    attn: MLAConfig
+    hidden_size: int = 7168
+    q_lora_rank: int = 1536
+    rope_theta: float = 50000.0
+    max_position: int = 131072
+    rms_eps: float = 1e-6
+    rope_scaling: Tuple[Tuple[str, Any], ...] | None = None  # e.g. (("rope_type", "yarn"), ("factor", 32.0), ...)
+    rope_interleaved: bool = True
+
+
+def yarn_mscale(factor: float, mscale: float) -> float:
+    """YaRN attention factor ``0.1 * mscale * ln(factor) + 1`` (1 for ``factor <= 1``)."""
+    return 1.0 if factor <= 1.0 else 0.1 * mscale * math.log(factor) + 1.0
+
+
+def softmax_mscale(rope_scaling) -> float:
+    """The factor whose square multiplies the softmax scale (1 without YaRN)."""
+    rs = dict(rope_scaling or ())
+    if rs.get("rope_type", rs.get("type")) != "yarn" or not rs.get("mscale_all_dim"):
+        return 1.0
+    return yarn_mscale(rs["factor"], rs["mscale_all_dim"])
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``x / sqrt(mean(x^2) + eps) * weight`` in fp32, cast back to ``x.dtype``."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+
+def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float, rope_scaling=None) -> torch.Tensor:
+    """``[max_position, rotary_dim]`` fp32: the cosines of the ``rotary_dim / 2`` frequencies, then the sines."""
+    half = rotary_dim // 2
+    inv_freq = 1.0 / (base ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))
+    rs = dict(rope_scaling or ())
+    kind = rs.get("rope_type", rs.get("type", "default"))
+    amp = 1.0
+    if kind == "yarn":
+        factor = float(rs["factor"])
+        orig = float(rs["original_max_position_embeddings"])
+
+        def dim_of(rotations: float) -> float:  # the dim index whose wavelength fits `rotations` turns in orig
+            return rotary_dim * math.log(orig / (rotations * 2 * math.pi)) / (2 * math.log(base))
+
+        lo = max(math.floor(dim_of(rs.get("beta_fast", 32.0))), 0)
+        hi = min(math.ceil(dim_of(rs.get("beta_slow", 1.0))), half - 1)
+        ramp = ((torch.arange(half, dtype=torch.float32) - lo) / max(hi - lo, 1)).clamp(0.0, 1.0)
+        inv_freq = inv_freq * (1.0 - ramp) + (inv_freq / factor) * ramp
+        if rs.get("mscale") is not None and rs.get("mscale_all_dim") is not None:
+            amp = yarn_mscale(factor, rs["mscale"]) / yarn_mscale(factor, rs["mscale_all_dim"])
+    elif kind != "default":
+        raise ValueError(f"unsupported rope scaling {kind!r}")
+    freqs = torch.arange(max_position, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    return torch.cat((freqs.cos() * amp, freqs.sin() * amp), dim=-1)
+
+
+def apply_rope(x: torch.Tensor, positions: torch.Tensor, cos_sin: torch.Tensor, interleaved: bool) -> torch.Tensor:
+    """RoPE on the last dim of ``x [T, ..., d]`` at ``positions [T]``, computed in fp32.
+
+    Pair ``i`` (``x[2i], x[2i+1]`` interleaved, ``x[i], x[i + d/2]`` otherwise) is rotated by
+    ``positions * inv_freq[i]``; the result keeps ``x``'s layout and dtype."""
+    d = x.shape[-1]
+    cs = cos_sin[positions.long()]
+    shape = (x.shape[0],) + (1,) * (x.dim() - 2) + (d // 2,)
+    cos, sin = cs[:, : d // 2].reshape(shape), cs[:, d // 2 :].reshape(shape)
+    xf = x.float()
+    if interleaved:
+        x1, x2 = xf[..., 0::2], xf[..., 1::2]
+        return torch.stack((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).flatten(-2).to(x.dtype)
+    x1, x2 = xf[..., : d // 2], xf[..., d // 2 :]
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+
+@dataclass
+class MLAWeights:
+    """Weights of one layer, ``[out_features, in_features]`` like torch.nn.Linear."""
+
+    q_a: torch.Tensor  # [q_lora_rank, hidden]
+    q_a_norm: torch.Tensor  # [q_lora_rank]
+    q_b: torch.Tensor  # [H * 192, q_lora_rank]
+    kv_a: torch.Tensor  # [512 + 64, hidden]
+    kv_a_norm: torch.Tensor  # [512]
+    kv_b: torch.Tensor  # [H * (128 + 128), 512]
+    o: torch.Tensor  # [hidden, H * 128]
+
+    @classmethod
+    def random(cls, cfg: MLALayerConfig, generator: torch.Generator, device, dtype=torch.bfloat16) -> "MLAWeights":
+        """Random-init weights of the layer's shapes (N(0, 1/fan_in); norm weights near 1)."""
+        a = cfg.attn
+        H = a.num_heads
+
+        def lin(out_f, in_f):
+            w = torch.randn((out_f, in_f), generator=generator) / math.sqrt(in_f)
+            return w.to(dtype).to(device)
+
+        def norm(n):
+            return (1.0 + 0.1 * torch.randn((n,), generator=generator)).to(dtype).to(device)
+
+        return cls(
+            q_a=lin(cfg.q_lora_rank, cfg.hidden_size),
+            q_a_norm=norm(cfg.q_lora_rank),
+            q_b=lin(H * a.qk_head_dim, cfg.q_lora_rank),
+            kv_a=lin(a.kv_dim, cfg.hidden_size),
+            kv_a_norm=norm(a.kv_lora_rank),
+            kv_b=lin(H * (a.qk_nope_head_dim + a.v_head_dim), a.kv_lora_rank),
+            o=lin(cfg.hidden_size, H * a.v_head_dim),
+        )
+
+    def w_uk(self, cfg: MLAConfig) -> torch.Tensor:
+        """``[H, 128, 512]`` view: ``k_nope = W_UK c``."""
+        w = self.kv_b.view(cfg.num_heads, cfg.qk_nope_head_dim + cfg.v_head_dim, cfg.kv_lora_rank)
+        return w[:, : cfg.qk_nope_head_dim]
+
+    def w_uv(self, cfg: MLAConfig) -> torch.Tensor:
+        """``[H, 128, 512]`` view: ``v = W_UV c``."""
+        w = self.kv_b.view(cfg.num_heads, cfg.qk_nope_head_dim + cfg.v_head_dim, cfg.kv_lora_rank)
+        return w[:, cfg.qk_nope_head_dim :]
+
+
+class MLAAttentionLayer:
+    def __init__(self, layer_id: int, cfg: MLALayerConfig, weights: MLAWeights) -> None:
+        a = cfg.attn
+        assert a.kv_lora_rank == 512 and a.qk_rope_head_dim == 64, "the HIP kernels take 512 + 64 latent rows"
+        assert abs(a.softmax_mscale - softmax_mscale(cfg.rope_scaling)) < 1e-12, (
+            "MLAConfig.softmax_mscale must be softmax_mscale(rope_scaling): the backend's scale comes from it"
+        )
+        self.layer_id = layer_id
+        self.cfg = cfg
+        self.w = weights
+        device = weights.q_a.device
+        self.cos_sin = rope_cos_sin_cache(a.qk_rope_head_dim, cfg.max_position, cfg.rope_theta, cfg.rope_scaling).to(
+            device
+        )
+        # absorption matrices, contiguous per head (batched products take no transposed views)
+        self.w_uk = weights.w_uk(a).contiguous()  # [H, 128, 512]
+        self.w_uv_t = weights.w_uv(a).transpose(1, 2).contiguous()  # [H, 512, 128]
+        self.w_uk_flat = self.w_uk.reshape(-1, a.kv_lora_rank)  # [H*128, 512]
+        self.w_uv_flat = weights.w_uv(a).reshape(-1, a.kv_lora_rank).contiguous()  # [H*128, 512]
+
+    def _decompress(self, c: torch.Tensor, k_pe: torch.Tensor):
+        """Per-head ``k [T, H, 192]`` and ``v [T, H, 128]`` of latents ``c [T, 512]``."""
+        a = self.cfg.attn
+        T = c.shape[0]
+        k_nope = (c @ self.w_uk_flat.t()).view(T, a.num_heads, a.qk_nope_head_dim)
+        v = (c @ self.w_uv_flat.t()).view(T, a.num_heads, a.v_head_dim)
+        k = torch.cat((k_nope, k_pe[:, None, :].expand(T, a.num_heads, a.qk_rope_head_dim)), dim=-1)
+        return k.contiguous(), v.contiguous()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """``x [T, hidden]`` (the tokens of ``ctx.batch``, in batch order) -> ``[T, hidden]``."""
+        a = self.cfg.attn
+        ctx = get_global_ctx()
+        batch, backend, pool = ctx.batch, ctx.attn_backend, ctx.kv_cache
+        T, H = x.shape[0], a.num_heads
+        eps, inter = self.cfg.rms_eps, self.cfg.rope_interleaved
+
+        q = (rms_norm(x @ self.w.q_a.t(), self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
+        kv = x @ self.w.kv_a.t()
+        c = rms_norm(kv[:, : a.kv_lora_rank], self.w.kv_a_norm, eps)
+        k_pe = apply_rope(kv[:, a.kv_lora_rank :], batch.positions, self.cos_sin, inter)
+        q_nope = q[..., : a.qk_nope_head_dim]
+        q_pe = apply_rope(q[..., a.qk_nope_head_dim :], batch.positions, self.cos_sin, inter)
+        latent = torch.cat((c, k_pe), dim=-1).contiguous()  # [T, 576]
+
+        if batch.is_decode:
+            # absorbed: q_lat[t, h] = q_nope[t, h] . W_UK[h]
+            q_lat = torch.bmm(q_nope.transpose(0, 1).contiguous(), self.w_uk).transpose(0, 1)  # [T, H, 512]
+            q_abs = torch.cat((q_lat, q_pe), dim=-1).contiguous()  # [T, H, 576]
+            if pool.has_prefill_pages:  # keep the per-head pages whole for a later prefill over this prefix
+                k, v = self._decompress(c, k_pe)
+                pool.store_kv(k, v, batch.out_loc, self.layer_id)
+            o_lat = backend.forward(q_abs, latent, None, self.layer_id, batch)  # stores the latent rows
+            o = torch.bmm(o_lat.transpose(0, 1).contiguous(), self.w_uv_t).transpose(0, 1)  # [T, H, 128]
+        else:
+            pool.store_kv(latent, None, batch.out_loc, self.layer_id)  # for the decode steps to come
+            k, v = self._decompress(c, k_pe)
+            # the backend stores k / v in the per-head pages, then attends over prefix + chunk
+            o = backend.forward(torch.cat((q_nope, q_pe), dim=-1).contiguous(), k, v, self.layer_id, batch)
+        return o.reshape(T, H * a.v_head_dim) @ self.w.o.t()

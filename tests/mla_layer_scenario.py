@@ -1,0 +1,78 @@
+"""A serving sequence for the MLA layer tests: chunked prefill, decode steps and a prefill
+continuing after decode, driven the way mini-sglang's scheduler drives a layer (a ``Batch`` with
+``positions`` / ``out_loc`` from the token table, ``prepare_metadata``, then ``forward`` inside
+``ctx.forward_batch``), and the oracle's output for every step."""
+
+from __future__ import annotations
+
+from typing import Dict, List, Sequence, Tuple
+
+import torch
+
+from minisgl_amd.core import Batch, Req
+from oracle import ref_mla_layer as RL
+
+# (phase, {request: new tokens}); decode steps extend every listed request by one token
+STEPS: List[Tuple[str, Dict[int, int]]] = [
+    ("prefill", {0: 40, 1: 25}),
+    ("prefill", {0: 30, 2: 17}),  # second chunk of request 0 over its 40-token prefix
+    ("decode", {0: 1, 1: 1, 2: 1}),
+    ("decode", {0: 1, 1: 1, 2: 1}),
+    ("prefill", {1: 20}),  # new input after decoding: attends the decoded tokens' K/V too
+    ("decode", {0: 1, 1: 1, 2: 1}),
+]
+
+
+def scaled_steps(factor: int) -> List[Tuple[str, Dict[int, int]]]:
+    return [(ph, {r: (e * factor if ph == "prefill" else e) for r, e in st.items()}) for ph, st in STEPS]
+
+
+def total_lens(steps) -> Dict[int, int]:
+    tot: Dict[int, int] = {}
+    for _, st in steps:
+        for r, e in st.items():
+            tot[r] = tot.get(r, 0) + e
+    return tot
+
+
+def token_table(lens: Dict[int, int], page_size: int, gen: torch.Generator, spare_pages: int = 2):
+    """Token table (one token location per column) over shuffled whole pages, and the page count."""
+    need = {r: -(-L // page_size) for r, L in lens.items()}
+    num_pages = sum(need.values()) + spare_pages
+    width = -(-max(n * page_size for n in need.values()) // 32) * 32
+    tt = torch.zeros((max(lens) + 2, width), dtype=torch.int32)
+    starts = torch.randperm(num_pages, generator=gen)[: sum(need.values())] * page_size
+    off = 0
+    for r, n in sorted(need.items()):
+        tt[r, : n * page_size] = (starts[off : off + n].unsqueeze(1) + torch.arange(page_size)).flatten().to(torch.int32)
+        off += n
+    return tt, num_pages
+
+
+def run(layer, ctx, backend, x_hist: Dict[int, torch.Tensor], steps, tt: torch.Tensor, device):
+    """Run ``steps`` through ``layer``; yields (phase, [(request, new tokens)], tokens per request
+    after the step, output [T, hidden])."""
+    cached = {r: 0 for r in x_hist}
+    for phase, st in steps:
+        order = sorted(st)
+        reqs = [Req(table_idx=r, cached_len=cached[r], device_len=cached[r] + st[r]) for r in order]
+        batch = Batch(reqs=reqs, phase=phase)
+        batch.padded_reqs = reqs
+        batch.positions = torch.cat([torch.arange(q.cached_len, q.device_len) for q in reqs]).to(torch.int32).to(device)
+        batch.out_loc = torch.cat([tt[q.table_idx, q.cached_len : q.device_len] for q in reqs]).to(device)
+        x = torch.cat([x_hist[r][cached[r] : cached[r] + st[r]] for r in order]).to(device)
+        backend.prepare_metadata(batch)
+        with ctx.forward_batch(batch):
+            out = layer.forward(x)
+        for r in order:
+            cached[r] += st[r]
+        yield phase, [(r, st[r]) for r in order], dict(cached), out
+
+
+def expected(x_hist, new: Sequence[Tuple[int, int]], cached_after: Dict[int, int], weights: dict, **kw):
+    """The oracle's output for one step, requests in batch order."""
+    outs = []
+    for r, e in new:
+        L = cached_after[r]
+        outs.append(RL.mla_layer(x_hist[r][:L], torch.arange(L), e, weights, **kw))
+    return torch.cat(outs)
