@@ -15,6 +15,10 @@ Prints one JSON line. ``value`` is the whole-step algorithmic HBM bandwidth
 dominant kernel (the split kernel) alone, 16 back-to-back launches per HIP
 graph, with HIP events on its launch stream.
 ``cpu_baseline`` times the CPU oracle on a bounded sample of the same batch.
+Extra fields: the prefill attention batch, a long-context batch, a mixed
+ragged batch, and ``layer``: whole Kimi-K2 MLA layer steps (projections,
+RoPE, absorption, attention kernels, o_proj) for the same decode and prefill
+batches (``--workload layer`` alone).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
 """
@@ -429,12 +433,71 @@ def bench_mixed(args):
     return res
 
 
+def bench_layer(args):
+    """Whole Kimi-K2-shape MLA layer steps (projections + RoPE + absorption + HIP attention + o_proj):
+    decode over the headline batch and prefill over the prefill batch, two layers alternating."""
+    import torch
+
+    from minisgl_amd.benchmark import layer as LB
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    res = {"workload": "Kimi-K2 MLA attention layer (H=64, hidden 7168, q_lora 1536, YaRN), projections through "
+           "hipBLASLt, attention through the HIP kernels; two layers alternate"}
+
+    lens = LB.decode_lens()
+    b = LB.LayerBench("decode", lens, [1] * len(lens), dev)
+    n = [0]
+
+    def dec_step():
+        b.step(n[0])
+        n[0] += 1
+
+    ms = _time_device(dec_step, stream, max(4, args.steps // 2), max(2, args.warmup // 2))
+    graphs = b.capture(stream)
+
+    def replay():
+        graphs[n[0] % 2].replay()
+        n[0] += 1
+
+    g_ms = _time_device(replay, stream, max(4, args.steps // 2), max(2, args.warmup // 2))
+    H = b.cfg.attn.num_heads
+    kv_bytes = sum(lens) * 576 * 2
+    attn_flops = sum(lens) * H * 2 * (576 + 512)
+    res["decode"] = {"batch": len(lens), "kv_tokens": sum(lens), "eager": LB.summary(b, ms, attn_flops, kv_bytes),
+                     "graph": LB.summary(b, g_ms, attn_flops, kv_bytes)}
+    del graphs
+    b.close()
+    del b
+    torch.cuda.empty_cache()
+
+    g = torch.Generator().manual_seed(0)
+    prefixes = torch.randint(0, 8193, (4,), generator=g).tolist()
+    extends = [2048] * 4
+    b = LB.LayerBench("prefill", [P + E for P, E in zip(prefixes, extends)], extends, dev)
+    n[0] = 0
+
+    def pre_step():
+        b.step(n[0])
+        n[0] += 1
+
+    ms = _time_device(pre_step, stream, max(2, args.steps // 10), max(2, args.warmup // 5))
+    attn_flops = sum(E * P + E * (E + 1) // 2 for E, P in zip(extends, prefixes)) * H * 2 * (192 + 128)
+    kv_bytes = sum(P + E for P, E in zip(prefixes, extends)) * H * (192 + 128) * 2
+    res["prefill"] = {"batch": 4, "prefixes": prefixes, "extend": 2048, **LB.summary(b, ms, attn_flops, kv_bytes)}
+    b.close()
+    del b
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed", "layer"])
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill summary of the decode line")
     ap.add_argument("--no-extra", action="store_true", help="skip the long-context and mixed-batch summaries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -443,7 +506,7 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part "
               "of this build", file=sys.stderr)
         sys.exit(2)
-    one = {"prefill": bench_prefill, "long": bench_long_context, "mixed": bench_mixed}
+    one = {"prefill": bench_prefill, "long": bench_long_context, "mixed": bench_mixed, "layer": bench_layer}
     if args.workload in one:
         print(json.dumps(one[args.workload](args)))
         return
@@ -453,6 +516,7 @@ def main():
     if not args.no_extra:
         res["long_context"] = bench_long_context(args)
         res["mixed"] = bench_mixed(args)
+        res["layer"] = bench_layer(args)
     print(json.dumps(res))
 
 

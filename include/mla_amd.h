@@ -181,6 +181,44 @@ int mla_prefill_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, cons
                      int64_t out_stride_t, int64_t out_stride_h, float *lse, int64_t lse_stride_t,
                      void *stream);
 
+/*
+ * The elementwise steps of the DeepSeek-V3 / Kimi-K2 MLA layer around the attention calls
+ * (bf16 in and out, fp32 arithmetic; strides in elements, multiples of 8; 16-byte aligned rows).
+ *
+ * mla_rmsnorm_bf16: out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * weight over n dims (n a multiple of
+ * 8), rows r < rows; out == x is allowed. Replaces the RMSNorm op of the layer (the reference's
+ * RMSNorm, python/minisgl/layers/norm.py, calls flashinfer's rmsnorm).
+ */
+int mla_rmsnorm_bf16(const void *x, int64_t x_row_stride, const void *weight, int32_t rows, int32_t n,
+                     float eps, void *out, int64_t out_row_stride, void *stream);
+
+/*
+ * mla_latent_rows_bf16: the latent row of each new token from the kv_a projection
+ * kv [rows, 576]: out[r][0:512] = rmsnorm(kv[r][0:512]) * norm_weight[512],
+ * out[r][512:576] = RoPE of kv[r][512:576] at positions[r]. cos_sin is the fp32 table
+ * [max_position, 64] (cosines of the 32 frequencies, then their sines; the layout of
+ * python/minisgl/layers/rotary.py:22-31); interleaved != 0 rotates pairs (2i, 2i+1), else
+ * (i, i + 32). Positions outside [0, max_position) are clamped into range. Replaces the norm +
+ * RotaryEmbedding.forward pair (rotary.py:39-51) for MLA's shared rope key.
+ */
+int mla_latent_rows_bf16(const void *kv, int64_t kv_row_stride, const void *norm_weight,
+                         const int32_t *positions, const float *cos_sin, int32_t max_position,
+                         int32_t rows, float eps, int32_t interleaved, void *out, int64_t out_row_stride,
+                         void *stream);
+
+/*
+ * mla_q_rope_bf16: queries q [tokens, heads, 192] (128 nope + 64 rope dims, strides
+ * (q_stride_t, q_stride_h)): pe_out[t, h, 0:64] = RoPE of q[t, h, 128:192] at positions[t]
+ * (pe_out may be q + 128 with q's strides: in place); if nope_out is not NULL,
+ * nope_out[t, h, 0:128] = q[t, h, 0:128] with its own strides (e.g. head-major for the W_UK
+ * absorption GEMM). RoPE conventions as mla_latent_rows_bf16. Replaces the query half of
+ * RotaryEmbedding.forward (rotary.py:39-51).
+ */
+int mla_q_rope_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, int32_t tokens, int32_t heads,
+                    const int32_t *positions, const float *cos_sin, int32_t max_position,
+                    int32_t interleaved, void *pe_out, int64_t pe_stride_t, int64_t pe_stride_h,
+                    void *nope_out, int64_t nope_stride_t, int64_t nope_stride_h, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 4; }
+int mla_abi_version(void) { return 5; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -421,6 +421,61 @@ int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   p.lse = lse;
   p.lse_stride_t = lse_stride_t;
   return hip_status(mla::launch_prefill(p, total_q, (hipStream_t)stream), "mla_prefill_bf16 launch");
+}
+
+static bool rows_ok(const void* p, int64_t stride, int64_t n) { return aligned(p, 16) && stride % 8 == 0 && stride >= n; }
+
+int mla_rmsnorm_bf16(const void* x, int64_t x_row_stride, const void* weight, int32_t rows, int32_t n, float eps,
+                     void* out, int64_t out_row_stride, void* stream) {
+  const char* who = "mla_rmsnorm_bf16";
+  if (rows < 0 || n <= 0 || n % 8 != 0) return fail(MLA_ERR_INVALID_ARG, "%s: rows %d, n %d (n a positive multiple of 8)", who, rows, n);
+  if (rows == 0) return ok();
+  if (x == nullptr || weight == nullptr || out == nullptr) return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!rows_ok(x, x_row_stride, n) || !rows_ok(out, out_row_stride, n) || !aligned(weight, 16))
+    return fail(MLA_ERR_INVALID_ARG, "%s: rows must be 16-byte aligned with strides multiples of 8 and >= n", who);
+  return hip_status(mla::launch_rmsnorm(x, x_row_stride, weight, out, out_row_stride, rows, n, eps, (hipStream_t)stream),
+                    "mla_rmsnorm_bf16 launch");
+}
+
+int mla_latent_rows_bf16(const void* kv, int64_t kv_row_stride, const void* norm_weight, const int32_t* positions,
+                         const float* cos_sin, int32_t max_position, int32_t rows, float eps, int32_t interleaved,
+                         void* out, int64_t out_row_stride, void* stream) {
+  const char* who = "mla_latent_rows_bf16";
+  if (rows < 0 || max_position <= 0) return fail(MLA_ERR_INVALID_ARG, "%s: rows %d, max_position %d", who, rows, max_position);
+  if (rows == 0) return ok();
+  if (kv == nullptr || norm_weight == nullptr || positions == nullptr || cos_sin == nullptr || out == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!rows_ok(kv, kv_row_stride, mla::kKvDim) || !rows_ok(out, out_row_stride, mla::kKvDim) || !aligned(norm_weight, 16))
+    return fail(MLA_ERR_INVALID_ARG, "%s: rows must be 16-byte aligned with strides multiples of 8 and >= 576", who);
+  return hip_status(mla::launch_latent_rows(kv, kv_row_stride, norm_weight, positions, cos_sin, max_position, out,
+                                            out_row_stride, rows, eps, interleaved, (hipStream_t)stream),
+                    "mla_latent_rows_bf16 launch");
+}
+
+int mla_q_rope_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, int32_t tokens, int32_t heads,
+                    const int32_t* positions, const float* cos_sin, int32_t max_position, int32_t interleaved,
+                    void* pe_out, int64_t pe_stride_t, int64_t pe_stride_h, void* nope_out, int64_t nope_stride_t,
+                    int64_t nope_stride_h, void* stream) {
+  const char* who = "mla_q_rope_bf16";
+  if (tokens < 0 || heads <= 0 || max_position <= 0)
+    return fail(MLA_ERR_INVALID_ARG, "%s: tokens %d, heads %d, max_position %d", who, tokens, heads, max_position);
+  if (tokens == 0) return ok();
+  if (q == nullptr || positions == nullptr || cos_sin == nullptr || pe_out == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!aligned(q, 16) || q_stride_t % 8 || q_stride_h % 8 || q_stride_h < 192 || q_stride_t < heads * q_stride_h)
+    return fail(MLA_ERR_INVALID_ARG, "%s: q must be 16-byte aligned, strides multiples of 8 holding %d heads of 192",
+                who, heads);
+  if (pe_stride_h < 64 || pe_stride_t < heads * pe_stride_h)
+    return fail(MLA_ERR_INVALID_ARG, "%s: pe_out strides (%lld, %lld) must hold %d heads of 64", who,
+                (long long)pe_stride_t, (long long)pe_stride_h, heads);
+  if (nope_out != nullptr && (!aligned(nope_out, 16) || nope_stride_t % 8 || nope_stride_h % 8 ||
+                              (nope_stride_t < nope_stride_h ? nope_stride_t : nope_stride_h) < 128))
+    return fail(MLA_ERR_INVALID_ARG, "%s: nope_out must be 16-byte aligned with strides multiples of 8 and >= 128",
+                who);
+  return hip_status(mla::launch_q_rope(q, q_stride_t, q_stride_h, tokens, heads, positions, cos_sin, max_position,
+                                       interleaved, pe_out, pe_stride_t, pe_stride_h, nope_out, nope_stride_t,
+                                       nope_stride_h, (hipStream_t)stream),
+                    "mla_q_rope_bf16 launch");
 }
 
 }  // extern "C"

@@ -106,5 +106,13 @@ hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stri
 hipError_t launch_page_table(const int32_t* tt, int32_t tt_rows, int64_t tt_stride, const int32_t* table_idx,
                              int32_t batch, int32_t cols, int32_t page_size, int32_t* out,
                              int64_t out_stride, hipStream_t stream);
+hipError_t launch_rmsnorm(const void* x, int64_t xs, const void* w, void* out, int64_t os, int32_t rows, int32_t n,
+                          float eps, hipStream_t stream);
+hipError_t launch_latent_rows(const void* kv, int64_t kvs, const void* w, const int32_t* pos, const float* cos_sin,
+                              int32_t max_pos, void* out, int64_t os, int32_t rows, float eps, int32_t interleaved,
+                              hipStream_t stream);
+hipError_t launch_q_rope(const void* q, int64_t qst, int64_t qsh, int32_t tokens, int32_t heads, const int32_t* pos,
+                         const float* cos_sin, int32_t max_pos, int32_t interleaved, void* pe, int64_t pst, int64_t psh,
+                         void* nope, int64_t nst, int64_t nsh, hipStream_t stream);
 
 }  // namespace mla

@@ -51,9 +51,17 @@ SIGNATURES = {
         [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, ctypes.c_float,
          _vp, _i64, _i64, _vp, _i64, _vp],
     ),
+    "mla_rmsnorm_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i64, _vp]),
+    "mla_latent_rows_bf16": (
+        ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _i32, _vp, _i64, _vp]
+    ),
+    "mla_q_rope_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp],
+    ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -250,4 +258,68 @@ def mla_prefill(q, k_pool, v_pool, page_table, cu_seqlens_q, seq_lens_k, scale: 
             0 if lse is None else lse.stride(0), _stream(stream),
         ),
         "mla_prefill_bf16",
+    )
+
+
+def rmsnorm(x, weight, eps: float, out=None, stream=None):
+    """``x [rows, n]`` bf16 -> ``x / sqrt(mean(x^2) + eps) * weight`` (``out`` may be ``x``)."""
+    import torch
+
+    assert x.dim() == 2 and x.dtype == torch.bfloat16 and x.stride(1) == 1 and x.is_cuda
+    rows, n = x.shape
+    assert weight.shape == (n,) and weight.dtype == torch.bfloat16 and weight.is_contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    assert out.shape == x.shape and out.dtype == torch.bfloat16 and out.stride(1) == 1
+    check(
+        load_library().mla_rmsnorm_bf16(_ptr(x), x.stride(0), _ptr(weight), rows, n, float(eps), _ptr(out),
+                                        out.stride(0), _stream(stream)),
+        "mla_rmsnorm_bf16",
+    )
+    return out
+
+
+def latent_rows(kv, norm_weight, positions, cos_sin, eps: float, interleaved: bool, out=None, stream=None):
+    """``kv [T, 576]`` (kv_a output) -> latent rows ``[T, 576]``: RMSNorm of the first 512 dims,
+    RoPE of the last 64 at ``positions`` (int32) from the fp32 ``cos_sin [max_position, 64]`` table."""
+    import torch
+
+    assert kv.dim() == 2 and kv.shape[1] == 576 and kv.dtype == torch.bfloat16 and kv.stride(1) == 1 and kv.is_cuda
+    T = kv.shape[0]
+    assert norm_weight.shape == (512,) and norm_weight.dtype == torch.bfloat16 and norm_weight.is_contiguous()
+    assert positions.shape == (T,) and positions.dtype == torch.int32 and positions.is_contiguous()
+    assert cos_sin.dim() == 2 and cos_sin.shape[1] == 64 and cos_sin.dtype == torch.float32 and cos_sin.is_contiguous()
+    if out is None:
+        out = torch.empty((T, 576), dtype=torch.bfloat16, device=kv.device)
+    assert out.shape == (T, 576) and out.dtype == torch.bfloat16 and out.stride(1) == 1
+    check(
+        load_library().mla_latent_rows_bf16(
+            _ptr(kv), kv.stride(0), _ptr(norm_weight), _ptr(positions), _ptr(cos_sin), cos_sin.shape[0], T,
+            float(eps), int(bool(interleaved)), _ptr(out), out.stride(0), _stream(stream),
+        ),
+        "mla_latent_rows_bf16",
+    )
+    return out
+
+
+def q_rope(q, positions, cos_sin, interleaved: bool, pe_out, nope_out=None, stream=None) -> None:
+    """``q [T, H, 192]``: ``pe_out [T, H, 64]`` = RoPE of the rope dims (may be ``q[..., 128:]``);
+    ``nope_out [T, H, 128]`` (any strides, e.g. a head-major buffer's transpose) = the nope dims."""
+    import torch
+
+    assert q.dim() == 3 and q.shape[2] == 192 and q.dtype == torch.bfloat16 and q.stride(2) == 1 and q.is_cuda
+    T, H, _ = q.shape
+    assert positions.shape == (T,) and positions.dtype == torch.int32 and positions.is_contiguous()
+    assert cos_sin.dim() == 2 and cos_sin.shape[1] == 64 and cos_sin.dtype == torch.float32 and cos_sin.is_contiguous()
+    assert pe_out.shape == (T, H, 64) and pe_out.dtype == torch.bfloat16 and pe_out.stride(2) == 1
+    if nope_out is not None:
+        assert nope_out.shape == (T, H, 128) and nope_out.dtype == torch.bfloat16 and nope_out.stride(2) == 1
+    check(
+        load_library().mla_q_rope_bf16(
+            _ptr(q), q.stride(0), q.stride(1), T, H, _ptr(positions), _ptr(cos_sin), cos_sin.shape[0],
+            int(bool(interleaved)), _ptr(pe_out), pe_out.stride(0), pe_out.stride(1), _ptr(nope_out),
+            0 if nope_out is None else nope_out.stride(0), 0 if nope_out is None else nope_out.stride(1),
+            _stream(stream),
+        ),
+        "mla_q_rope_bf16",
     )

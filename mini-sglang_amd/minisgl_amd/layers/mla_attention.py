@@ -30,8 +30,10 @@ reference's MHA models rotate halves ``(i, i + d/2)``. YaRN also scales the soft
 attention factor as DeepSeek-V3 applies it), carried by ``MLAConfig.softmax_mscale`` so that
 the backend's scale agrees.
 
-The GEMMs are plain library GEMMs (torch.matmul / bmm on hipBLASLt); the attention is the HIP
-library. Tensor-parallel sharding is out of scope (one GPU): ``num_heads`` is this rank's.
+The GEMMs are plain library GEMMs (torch.matmul / bmm on hipBLASLt); the elementwise steps
+(RMSNorm, the latent row = norm + RoPE, the queries' RoPE and head-major nope copy) and the
+attention are the HIP library (``HipLayerOps``, ``minisgl_amd.kernel.lib``). Tensor-parallel
+sharding is out of scope (one GPU): ``num_heads`` is this rank's.
 """
 
 from __future__ import annotations
@@ -44,6 +46,7 @@ import torch
 
 from ..config import MLAConfig
 from ..core import get_global_ctx
+from ..kernel import lib
 
 
 @dataclass(frozen=True)
@@ -69,12 +72,6 @@ def softmax_mscale(rope_scaling) -> float:
     if rs.get("rope_type", rs.get("type")) != "yarn" or not rs.get("mscale_all_dim"):
         return 1.0
     return yarn_mscale(rs["factor"], rs["mscale_all_dim"])
-
-
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``x / sqrt(mean(x^2) + eps) * weight`` in fp32, cast back to ``x.dtype``."""
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
 
 
 def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float, rope_scaling=None) -> torch.Tensor:
@@ -103,21 +100,25 @@ def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float, rope_sca
     return torch.cat((freqs.cos() * amp, freqs.sin() * amp), dim=-1)
 
 
-def apply_rope(x: torch.Tensor, positions: torch.Tensor, cos_sin: torch.Tensor, interleaved: bool) -> torch.Tensor:
-    """RoPE on the last dim of ``x [T, ..., d]`` at ``positions [T]``, computed in fp32.
+class HipLayerOps:
+    """The layer's elementwise steps on the HIP kernels (bf16 device tensors only; no fallback).
 
-    Pair ``i`` (``x[2i], x[2i+1]`` interleaved, ``x[i], x[i + d/2]`` otherwise) is rotated by
-    ``positions * inv_freq[i]``; the result keeps ``x``'s layout and dtype."""
-    d = x.shape[-1]
-    cs = cos_sin[positions.long()]
-    shape = (x.shape[0],) + (1,) * (x.dim() - 2) + (d // 2,)
-    cos, sin = cs[:, : d // 2].reshape(shape), cs[:, d // 2 :].reshape(shape)
-    xf = x.float()
-    if interleaved:
-        x1, x2 = xf[..., 0::2], xf[..., 1::2]
-        return torch.stack((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).flatten(-2).to(x.dtype)
-    x1, x2 = xf[..., : d // 2], xf[..., d // 2 :]
-    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+    ``rms_norm(x, w, eps)`` normalises the rows of a fresh projection output in place;
+    ``latent_rows(kv, w, positions, cos_sin, eps, interleaved)`` -> ``[T, 576]``;
+    ``q_rope(q, positions, cos_sin, interleaved, pe_out, nope_out=None)`` writes the roped rope
+    dims to ``pe_out`` (possibly in place) and, if given, the nope dims to ``nope_out``."""
+
+    @staticmethod
+    def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+        return lib.rmsnorm(x, w, eps, out=x)
+
+    @staticmethod
+    def latent_rows(kv, w, positions, cos_sin, eps: float, interleaved: bool) -> torch.Tensor:
+        return lib.latent_rows(kv, w, positions, cos_sin, eps, interleaved)
+
+    @staticmethod
+    def q_rope(q, positions, cos_sin, interleaved: bool, pe_out, nope_out=None) -> None:
+        lib.q_rope(q, positions, cos_sin, interleaved, pe_out, nope_out)
 
 
 @dataclass
@@ -167,7 +168,7 @@ class MLAWeights:
 
 
 class MLAAttentionLayer:
-    def __init__(self, layer_id: int, cfg: MLALayerConfig, weights: MLAWeights) -> None:
+    def __init__(self, layer_id: int, cfg: MLALayerConfig, weights: MLAWeights, ops=None) -> None:
         a = cfg.attn
         assert a.kv_lora_rank == 512 and a.qk_rope_head_dim == 64, "the HIP kernels take 512 + 64 latent rows"
         assert abs(a.softmax_mscale - softmax_mscale(cfg.rope_scaling)) < 1e-12, (
@@ -176,6 +177,7 @@ class MLAAttentionLayer:
         self.layer_id = layer_id
         self.cfg = cfg
         self.w = weights
+        self.ops = ops if ops is not None else HipLayerOps()
         device = weights.q_a.device
         self.cos_sin = rope_cos_sin_cache(a.qk_rope_head_dim, cfg.max_position, cfg.rope_theta, cfg.rope_scaling).to(
             device
@@ -186,14 +188,15 @@ class MLAAttentionLayer:
         self.w_uk_flat = self.w_uk.reshape(-1, a.kv_lora_rank)  # [H*128, 512]
         self.w_uv_flat = weights.w_uv(a).reshape(-1, a.kv_lora_rank).contiguous()  # [H*128, 512]
 
-    def _decompress(self, c: torch.Tensor, k_pe: torch.Tensor):
-        """Per-head ``k [T, H, 192]`` and ``v [T, H, 128]`` of latents ``c [T, 512]``."""
+    def _decompress(self, latent: torch.Tensor):
+        """Per-head ``k [T, H, 192]`` and ``v [T, H, 128]`` of latent rows ``[T, 576]``."""
         a = self.cfg.attn
-        T = c.shape[0]
+        T = latent.shape[0]
+        c = latent[:, : a.kv_lora_rank]
         k_nope = (c @ self.w_uk_flat.t()).view(T, a.num_heads, a.qk_nope_head_dim)
         v = (c @ self.w_uv_flat.t()).view(T, a.num_heads, a.v_head_dim)
-        k = torch.cat((k_nope, k_pe[:, None, :].expand(T, a.num_heads, a.qk_rope_head_dim)), dim=-1)
-        return k.contiguous(), v.contiguous()
+        k_pe = latent[:, None, a.kv_lora_rank :].expand(T, a.num_heads, a.qk_rope_head_dim)
+        return torch.cat((k_nope, k_pe), dim=-1), v
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """``x [T, hidden]`` (the tokens of ``ctx.batch``, in batch order) -> ``[T, hidden]``."""
@@ -201,28 +204,27 @@ class MLAAttentionLayer:
         ctx = get_global_ctx()
         batch, backend, pool = ctx.batch, ctx.attn_backend, ctx.kv_cache
         T, H = x.shape[0], a.num_heads
-        eps, inter = self.cfg.rms_eps, self.cfg.rope_interleaved
+        ops, eps, inter = self.ops, self.cfg.rms_eps, self.cfg.rope_interleaved
+        pos = batch.positions.to(torch.int32)  # no copy when the scheduler already gives int32
 
-        q = (rms_norm(x @ self.w.q_a.t(), self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
-        kv = x @ self.w.kv_a.t()
-        c = rms_norm(kv[:, : a.kv_lora_rank], self.w.kv_a_norm, eps)
-        k_pe = apply_rope(kv[:, a.kv_lora_rank :], batch.positions, self.cos_sin, inter)
-        q_nope = q[..., : a.qk_nope_head_dim]
-        q_pe = apply_rope(q[..., a.qk_nope_head_dim :], batch.positions, self.cos_sin, inter)
-        latent = torch.cat((c, k_pe), dim=-1).contiguous()  # [T, 576]
+        q = (ops.rms_norm(x @ self.w.q_a.t(), self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
+        latent = ops.latent_rows(x @ self.w.kv_a.t(), self.w.kv_a_norm, pos, self.cos_sin, eps, inter)  # [T, 576]
 
         if batch.is_decode:
-            # absorbed: q_lat[t, h] = q_nope[t, h] . W_UK[h]
-            q_lat = torch.bmm(q_nope.transpose(0, 1).contiguous(), self.w_uk).transpose(0, 1)  # [T, H, 512]
-            q_abs = torch.cat((q_lat, q_pe), dim=-1).contiguous()  # [T, H, 576]
+            # absorbed: q_abs = [q_nope W_UK | rope(q_pe)] per head; the nope dims go head-major for the bmm
+            q_abs = torch.empty((T, H, a.kv_dim), dtype=x.dtype, device=x.device)
+            q_nope_h = torch.empty((H, T, a.qk_nope_head_dim), dtype=x.dtype, device=x.device)
+            ops.q_rope(q, pos, self.cos_sin, inter, q_abs[..., a.kv_lora_rank :], q_nope_h.transpose(0, 1))
+            q_abs[..., : a.kv_lora_rank] = torch.bmm(q_nope_h, self.w_uk).transpose(0, 1)
             if pool.has_prefill_pages:  # keep the per-head pages whole for a later prefill over this prefix
-                k, v = self._decompress(c, k_pe)
+                k, v = self._decompress(latent)
                 pool.store_kv(k, v, batch.out_loc, self.layer_id)
             o_lat = backend.forward(q_abs, latent, None, self.layer_id, batch)  # stores the latent rows
             o = torch.bmm(o_lat.transpose(0, 1).contiguous(), self.w_uv_t).transpose(0, 1)  # [T, H, 128]
         else:
             pool.store_kv(latent, None, batch.out_loc, self.layer_id)  # for the decode steps to come
-            k, v = self._decompress(c, k_pe)
+            ops.q_rope(q, pos, self.cos_sin, inter, q[..., a.qk_nope_head_dim :])  # in place
+            k, v = self._decompress(latent)
             # the backend stores k / v in the per-head pages, then attends over prefix + chunk
-            o = backend.forward(torch.cat((q_nope, q_pe), dim=-1).contiguous(), k, v, self.layer_id, batch)
+            o = backend.forward(q, k, v, self.layer_id, batch)
         return o.reshape(T, H * a.v_head_dim) @ self.w.o.t()

@@ -23,6 +23,40 @@ STEPS: List[Tuple[str, Dict[int, int]]] = [
 ]
 
 
+class TorchLayerOps:
+    """fp32 torch versions of the layer's elementwise steps (``HipLayerOps``' contract), for
+    running the layer's glue on the CPU and as the GPU kernels' fp32 reference."""
+
+    @staticmethod
+    def rms_norm(x, w, eps):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
+
+    @staticmethod
+    def rope(x, positions, cos_sin, interleaved):
+        d = x.shape[-1]
+        cs = cos_sin[positions.long()]
+        shape = (x.shape[0],) + (1,) * (x.dim() - 2) + (d // 2,)
+        cos, sin = cs[:, : d // 2].reshape(shape), cs[:, d // 2 :].reshape(shape)
+        xf = x.float()
+        if interleaved:
+            x1, x2 = xf[..., 0::2], xf[..., 1::2]
+            return torch.stack((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).flatten(-2).to(x.dtype)
+        x1, x2 = xf[..., : d // 2], xf[..., d // 2 :]
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    @classmethod
+    def latent_rows(cls, kv, w, positions, cos_sin, eps, interleaved):
+        return torch.cat((cls.rms_norm(kv[:, :512], w, eps), cls.rope(kv[:, 512:], positions, cos_sin, interleaved)),
+                         dim=-1)
+
+    @classmethod
+    def q_rope(cls, q, positions, cos_sin, interleaved, pe_out, nope_out=None):
+        pe_out.copy_(cls.rope(q[..., 128:], positions, cos_sin, interleaved))
+        if nope_out is not None:
+            nope_out.copy_(q[..., :128])
+
+
 def scaled_steps(factor: int) -> List[Tuple[str, Dict[int, int]]]:
     return [(ph, {r: (e * factor if ph == "prefill" else e) for r, e in st.items()}) for ph, st in STEPS]
 

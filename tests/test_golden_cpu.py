@@ -63,3 +63,25 @@ def test_host_errors_are_reported():
     buf = (ctypes.c_int32 * 16)()
     rc = so.mla_decode_plan(lens, 1, 48, 4, 1024, buf, buf, ctypes.byref(ctypes.c_int32()))
     assert rc == 1 and b"power of two" in so.mla_last_error()
+
+
+def test_layer_op_argument_errors_are_reported():
+    """The layer ops' C-ABI checks reject bad shapes and strides before any device work."""
+    from minisgl_amd.kernel import lib
+
+    so = lib.load_library()
+    buf = ctypes.create_string_buffer(64 * 1024 + 16)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16  # 16-byte aligned host address, never dereferenced
+    rc = so.mla_rmsnorm_bf16(p, 512, p, 2, 7, 1e-6, p, 512, None)
+    assert rc != 0 and b"multiple of 8" in so.mla_last_error()
+    rc = so.mla_rmsnorm_bf16(p, 500, p, 2, 512, 1e-6, p, 512, None)
+    assert rc != 0 and b"strides" in so.mla_last_error()
+    rc = so.mla_latent_rows_bf16(p, 576, p, p, p, 0, 4, 1e-6, 1, p, 576, None)
+    assert rc != 0 and b"max_position" in so.mla_last_error()
+    rc = so.mla_latent_rows_bf16(p, 512, p, p, p, 16, 4, 1e-6, 1, p, 576, None)
+    assert rc != 0 and b">= 576" in so.mla_last_error()
+    rc = so.mla_q_rope_bf16(p, 192, 192, 4, 2, p, p, 16, 1, p, 128, 64, None, 0, 0, None)
+    assert rc != 0 and b"heads of 192" in so.mla_last_error()
+    rc = so.mla_q_rope_bf16(p, 384, 192, 4, 2, p, p, 16, 1, p, 128, 64, p + 2, 128, 512, None)
+    assert rc != 0 and b"nope_out" in so.mla_last_error()
+    assert so.mla_rmsnorm_bf16(None, 0, None, 0, 8, 1e-6, None, 0, None) == 0  # no rows: nothing to do

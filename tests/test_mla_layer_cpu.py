@@ -26,15 +26,7 @@ import torch
 
 from minisgl_amd.config import MLAConfig
 from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
-from minisgl_amd.layers import (
-    MLAAttentionLayer,
-    MLALayerConfig,
-    MLAWeights,
-    apply_rope,
-    rms_norm,
-    rope_cos_sin_cache,
-    softmax_mscale,
-)
+from minisgl_amd.layers import MLAAttentionLayer, MLALayerConfig, MLAWeights, rope_cos_sin_cache, softmax_mscale
 from oracle import ref_mla as R
 from oracle import ref_mla_layer as RL
 
@@ -159,27 +151,45 @@ def test_yarn_closed_forms():
 
 
 @pytest.mark.parametrize("scaling", [None, KIMI_YARN, DSV3_YARN])
-@pytest.mark.parametrize("interleaved", [True, False])
-def test_product_rope_matches_oracle(scaling, interleaved):
-    gen = torch.Generator().manual_seed(7)
-    cache = rope_cos_sin_cache(64, 8192, 50000.0, scaling)
+def test_product_cos_sin_cache_matches_oracle(scaling):
+    """The layer's fp32 cos/sin table against the oracle's float64 angles (rotary.py:27-31 builds
+    the table in fp32 the same way: position x inv_freq, then cos and sin)."""
+    cache = rope_cos_sin_cache(64, 8192, 50000.0, scaling).double()
     inv, amp = RL.rope_inv_freq(64, 50000.0, dict(scaling or ()))
+    ang = torch.arange(8192, dtype=torch.float64)[:, None] * inv[None, :]
+    torch.testing.assert_close(cache[:, :32], ang.cos() * amp, atol=2e-3, rtol=0)
+    torch.testing.assert_close(cache[:, 32:], ang.sin() * amp, atol=2e-3, rtol=0)
+    torch.testing.assert_close(cache[:100, :32], ang[:100].cos() * amp, atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_torch_layer_ops_match_oracle(interleaved):
+    """The fp32 torch ops that stand in for the HIP ones on the CPU (and are the GPU kernels'
+    fp32 reference) against the oracle's float64 rope / RMSNorm."""
+    gen = torch.Generator().manual_seed(7)
+    cache = rope_cos_sin_cache(64, 8192, 50000.0, KIMI_YARN)
+    inv, amp = RL.rope_inv_freq(64, 50000.0, dict(KIMI_YARN))
     pos = torch.randint(0, 8192, (33,), generator=gen)
-    x = torch.randn((33, 5, 64), generator=gen)
-    got = apply_rope(x, pos, cache, interleaved)
-    want = RL.rope(x.double(), pos, inv, amp, interleaved)
-    # the cache holds fp32 angles (pos * inv_freq), as rotary.py:27-31 builds it
-    torch.testing.assert_close(got.double(), want, atol=5e-3, rtol=0)
+    kv = torch.randn((33, 576), generator=gen)
+    w = 1 + 0.1 * torch.randn(512, generator=gen)
+    got = S.TorchLayerOps.latent_rows(kv, w, pos, cache, 1e-6, interleaved).double()
+    torch.testing.assert_close(got[:, :512], RL.rms_norm(kv[:, :512].double(), w.double(), 1e-6), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(got[:, 512:], RL.rope(kv[:, 512:].double(), pos, inv, amp, interleaved), atol=5e-3,
+                               rtol=0)
+    q = torch.randn((33, 5, 192), generator=gen)
+    pe, nope = torch.empty((33, 5, 64)), torch.empty((5, 33, 128))
+    S.TorchLayerOps.q_rope(q, pos, cache, interleaved, pe, nope.transpose(0, 1))
+    torch.testing.assert_close(pe.double(), RL.rope(q[..., 128:].double(), pos, inv, amp, interleaved), atol=5e-3,
+                               rtol=0)
+    assert torch.equal(nope.transpose(0, 1), q[..., :128])
 
 
-def test_rms_norm_closed_form_and_oracle():
+def test_rms_norm_closed_form():
     x = torch.full((3, 512), 0.25)
     w = torch.linspace(0.5, 1.5, 512)
-    torch.testing.assert_close(rms_norm(x, w, 1e-6), (w * 0.25 / math.sqrt(0.0625 + 1e-6)).expand(3, 512))
-    gen = torch.Generator().manual_seed(8)
-    y = torch.randn((4, 512), generator=gen) * 3
-    torch.testing.assert_close(rms_norm(y, w, 1e-6).double(), RL.rms_norm(y.double(), w.double(), 1e-6), atol=1e-5,
-                               rtol=1e-5)
+    want = (w * 0.25 / math.sqrt(0.0625 + 1e-6)).expand(3, 512)
+    torch.testing.assert_close(S.TorchLayerOps.rms_norm(x, w, 1e-6), want)
+    torch.testing.assert_close(RL.rms_norm(x.double(), w.double(), 1e-6), want.double())
 
 
 # ---------------------------------------------------------------- product layer on a CPU stand-in
@@ -243,7 +253,7 @@ def test_product_layer_on_dense_stand_in(scaling):
     cfg = MLALayerConfig(attn=attn, hidden_size=64, q_lora_rank=48, rope_theta=50000.0, max_position=4096,
                          rope_scaling=scaling)
     weights = MLAWeights.random(cfg, gen, "cpu", dtype=torch.float32)
-    layer = MLAAttentionLayer(0, cfg, weights)
+    layer = MLAAttentionLayer(0, cfg, weights, ops=S.TorchLayerOps())
     lens = S.total_lens(S.STEPS)
     tt, num_pages = S.token_table(lens, 16, gen)
     ctx = Context(page_size=16)

@@ -77,3 +77,55 @@ def test_mla_layer_kimi_k2_shape():
     """64 heads (Kimi-K2 / DeepSeek-V3 with 1 or 2 way head sharding), hidden 7168, q_lora 1536."""
     steps = [("prefill", {0: 150, 1: 66}), ("decode", {0: 1, 1: 1}), ("prefill", {0: 70}), ("decode", {0: 1, 1: 1})]
     _run_case(H=64, hidden=7168, q_lora=1536, steps=steps, seed=1)
+
+
+def test_mla_layer_decode_graph_replay():
+    """A decode layer step captured in a HIP graph and replayed (with eager work between replays)
+    gives the eager step's output every time."""
+    reset_global_ctx()
+    gen = torch.Generator().manual_seed(3)
+    H, hidden = 64, 1024
+    attn = MLAConfig(num_heads=H, num_layers=1, softmax_mscale=softmax_mscale(KIMI_YARN))
+    cfg = MLALayerConfig(attn=attn, hidden_size=hidden, q_lora_rank=384, rope_theta=50000.0, max_position=16384,
+                         rope_scaling=KIMI_YARN)
+    weights = MLAWeights.random(cfg, gen, DEV)
+    steps = [("prefill", {0: 300, 1: 70, 2: 129}), ("decode", {0: 1, 1: 1, 2: 1})]
+    lens = S.total_lens(steps)
+    tt, num_pages = S.token_table(lens, 64, gen)
+    ctx = Context(page_size=64)
+    set_global_ctx(ctx)
+    ctx.page_table = tt.to(DEV)
+    ctx.kv_cache = create_kvcache_pool(attn, num_pages, 64, torch.bfloat16, DEV, with_prefill_pages=True)
+    backend = create_attention_backend("mla", attn)
+    ctx.attn_backend = backend
+    layer = MLAAttentionLayer(0, cfg, weights)
+    x_hist = {r: torch.randn((L, hidden), generator=gen).to(torch.bfloat16) for r, L in lens.items()}
+    try:
+        outs = [out for *_, out in S.run(layer, ctx, backend, x_hist, steps, tt, DEV)]
+        eager = outs[-1].clone()
+        # the same decode step again, as a graph: batch tensors are the static inputs
+        from minisgl_amd.core import Batch, Req
+
+        reqs = [Req(table_idx=r, cached_len=lens[r] - 1, device_len=lens[r]) for r in sorted(lens)]
+        batch = Batch(reqs=reqs, phase="decode")
+        batch.padded_reqs = reqs
+        batch.positions = torch.tensor([lens[r] - 1 for r in sorted(lens)], dtype=torch.int32, device=DEV)
+        batch.out_loc = torch.stack([tt[r, lens[r] - 1] for r in sorted(lens)]).to(DEV)
+        x = torch.stack([x_hist[r][lens[r] - 1] for r in sorted(lens)]).to(DEV)
+        backend.prepare_metadata(batch)
+        stream = torch.cuda.Stream()
+        with ctx.forward_batch(batch), torch.cuda.stream(stream):
+            layer.forward(x)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                static_out = layer.forward(x)
+        torch.cuda.synchronize()
+        for i in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            print(f"[mla layer graph] replay {i}: max diff {float((static_out - eager).abs().max()):.3e}", flush=True)
+            torch.testing.assert_close(static_out.float(), eager.float(), atol=1e-2, rtol=1e-2)
+            _ = (x.float() * 2).sum().item()  # eager work between replays
+    finally:
+        reset_global_ctx()
