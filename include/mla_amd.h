@@ -112,7 +112,7 @@ int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
  *            ws_lse [ws_slots, heads] fp32
  *   out      [batch, heads, 512] strides (out_stride_b, out_stride_h)
  *   lse      [batch, heads] fp32 (row stride lse_stride_b) or NULL
- * heads is 16, 32, 48 or 64 (one wave per 16 heads); page_size a power of
+ * heads is 1..64 (one wave per 16 heads; the last wave's lanes beyond `heads` idle); page_size a power of
  * two; page ids outside [0, num_pages) are clamped into range.
  * Launches the split kernel on num_ctas CTAs, then the LSE merge kernel.
  */

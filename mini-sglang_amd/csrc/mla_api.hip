@@ -247,8 +247,7 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
                          int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, void* ws_o,
                          float* ws_lse, int32_t ws_slots, void* out, int64_t out_stride_b, int64_t out_stride_h,
                          float* lse, int64_t lse_stride_b, mla::DecodeParams* p) {
-  if (heads != 16 && heads != 32 && heads != 48 && heads != 64)
-    return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be 16, 32, 48 or 64, got %d", who, heads);
+  if (heads < 1 || heads > 64) return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be in [1, 64], got %d", who, heads);
   if (q == nullptr || kv_pool == nullptr || page_table == nullptr || seq_lens == nullptr || plan == nullptr)
     return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
   if (!aligned(q, 16) || q_stride_h % 8 != 0 || q_stride_b % 8 != 0 || q_stride_h < MLA_KV_DIM ||

@@ -94,11 +94,17 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     const int slot_base = req_info[3 * b + 2];
 
     // ---- Q^T operand (B of the QK MFMA): head c of this wave, dims ks*32 + 8g .. +8
+    // A head count that is not a multiple of 16 leaves lanes of the last wave without a head:
+    // they compute with a zero query (read from head 0's row, always in bounds) and store nothing.
     const int h = wave * 16 + c;
-    const __bf16* qrow = p.q + (int64_t)b * p.q_stride_b + (int64_t)h * p.q_stride_h + g * 8;
+    const bool h_ok = h < p.heads;
+    const __bf16* qrow = p.q + (int64_t)b * p.q_stride_b + (int64_t)(h_ok ? h : 0) * p.q_stride_h + g * 8;
     bf16x8 qf[18];
 #pragma unroll
-    for (int ks = 0; ks < 18; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
+    for (int ks = 0; ks < 18; ++ks) {
+      qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + ks * 32);
+      if (!h_ok) qf[ks] = bf16x8{};
+    }
     // Consume Q here so the compiler's vmcnt wait for these loads lands before
     // the tile loop; at their first use inside the loop it would also wait for
     // every DMA load in flight (the counter is in order) on every tile.
@@ -268,7 +274,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     const float l_tot = wave_sum_g(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const float lse_nat = l_tot > 0.f ? (m_ref + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
-    if (npieces == 1) {
+    if (!h_ok) {
+      // no head on this lane
+    } else if (npieces == 1) {
       __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 4 * g;
 #pragma unroll
       for (int db = 0; db < 32; ++db) {
@@ -382,7 +390,7 @@ hipError_t launch_decode_nw(const DecodeParams& p, hipStream_t stream) {
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
   if (p.heads == 64 && p.log2_ps >= 5) return launch_decode_stream(p, stream);
-  switch (p.heads / 16) {
+  switch ((p.heads + 15) / 16) {
     case 1: return launch_decode_nw<1>(p, stream);
     case 2: return launch_decode_nw<2>(p, stream);
     case 3: return launch_decode_nw<3>(p, stream);

@@ -70,6 +70,31 @@ def test_decode_heads_and_page_sizes(heads, ps):
     check_case(case, 64)
 
 
+@pytest.mark.parametrize("heads,ps", [(1, 64), (8, 64), (8, 16), (20, 32), (63, 128)])
+def test_decode_tensor_parallel_head_counts(heads, ps):
+    """Head counts that are not a multiple of 16 (a tensor-parallel shard: Kimi-K2 over 8 GPUs has
+    8 heads per GPU): the last wave's lanes without a head compute nothing that is stored."""
+    print(f"[decode heads] heads={heads} ps={ps}", flush=True)
+    case = make_decode_case(6, heads, ps, lens=[1, 64, 65, 700, 2048, 33], seed=heads * 7 + ps)
+    check_case(case, 64)
+    check_case(case, 3)
+    # outputs inside a wider buffer: the head slot past `heads` must stay untouched
+    B = len(case.lens)
+    plan_np, slots = lib.decode_plan(case.lens, ps, 3)
+    plan = torch.from_numpy(plan_np).to(DEV)
+    ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.bfloat16, device=DEV)
+    ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
+    wide = torch.full((B, heads + 1, 512), 7.0, dtype=torch.bfloat16, device=DEV)
+    wide_lse = torch.full((B, heads + 1), 7.0, dtype=torch.float32, device=DEV)
+    lib.mla_decode(case.q.to(DEV), case.kv_pool.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV), plan, 3,
+                   ws_o, ws_lse, R.DEFAULT_SCALE, wide[:, :heads], wide_lse[:, :heads])
+    torch.cuda.synchronize()
+    assert torch.all(wide[:, heads] == 7.0) and torch.all(wide_lse[:, heads] == 7.0)
+    o_ref, lse_ref = R.mla_decode(case.q, case.kv_pool, case.page_table, case.lens)
+    torch.testing.assert_close(wide[:, :heads].float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(wide_lse[:, :heads].cpu(), lse_ref, **LSE_TOL)
+
+
 def test_decode_long_split_merge():
     """Long requests split over many CTAs exercise the LSE merge kernel."""
     case = make_decode_case(3, 64, 64, lens=[20000, 4097, 130], seed=3)

@@ -79,6 +79,12 @@ def test_mla_layer_kimi_k2_shape():
     _run_case(H=64, hidden=7168, q_lora=1536, steps=steps, seed=1)
 
 
+def test_mla_layer_kimi_k2_tp8_shard():
+    """Kimi-K2's attention over 8 GPUs: 8 heads per GPU, hidden 7168."""
+    steps = [("prefill", {0: 90, 1: 40}), ("decode", {0: 1, 1: 1}), ("decode", {0: 1, 1: 1})]
+    _run_case(H=8, hidden=7168, q_lora=1536, steps=steps, seed=2)
+
+
 def test_mla_layer_decode_graph_replay():
     """A decode layer step captured in a HIP graph and replayed (with eager work between replays)
     gives the eager step's output every time."""
