@@ -112,7 +112,10 @@ int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
  *            ws_lse [ws_slots, heads] fp32
  *   out      [batch, heads, 512] strides (out_stride_b, out_stride_h)
  *   lse      [batch, heads] fp32 (row stride lse_stride_b) or NULL
- * heads is 1..64 (one wave per 16 heads; the last wave's lanes beyond `heads` idle); page_size a power of
+ * heads is 1..1024: groups of at most 64 heads run one after another (each group reads the KV
+ * again) and group g's partials occupy the workspace block [ws_slots, group heads, 512] that
+ * starts at ws_o + ws_slots * 64 * g * 512 (ws_lse likewise), so a [ws_slots, heads, 512] buffer
+ * holds them all; within a group, one wave per 16 heads (lanes past `heads` idle). page_size a power of
  * two; page ids outside [0, num_pages) are clamped into range.
  * Launches the split kernel on num_ctas CTAs, then the LSE merge kernel.
  */
@@ -146,7 +149,8 @@ int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
  *   lse = ln sum_i exp(ws_lse[s_i]);  out = sum_i exp(ws_lse[s_i] - lse) * ws_o[s_i]
  * n == 0 writes out = 0, lse = -inf. With single_piece_final != 0 requests
  * with n == 1 are skipped (the split step already wrote them); otherwise
- * their one slot is converted like any other.
+ * their one slot is converted like any other. More than 64 heads: the workspace holds one
+ * [ws_slots, group heads, 512] block per 64-head group, as mla_decode_bf16 writes it.
  */
 int mla_decode_merge_f32(const void *ws_o, const float *ws_lse, int32_t ws_slots,
                          const int32_t *req_info, int32_t batch, int32_t heads,

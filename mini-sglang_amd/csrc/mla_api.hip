@@ -311,6 +311,42 @@ static mla::MergeParams merge_params(const void* ws_o, const float* ws_lse, int3
   return m;
 }
 
+// Decode runs in groups of at most 64 query heads (one streaming-kernel CTA holds 64 heads' state);
+// a group's partials occupy its own [ws_slots, group heads, 512] block of the workspace, so the
+// caller's [ws_slots, heads, 512] buffer holds every group's block back to back.
+constexpr int32_t kHeadGroup = 64;
+constexpr int32_t kMaxHeads = 1024;
+
+struct HeadGroup {
+  const void* q;
+  void* ws_o;
+  float* ws_lse;
+  void* out;
+  float* lse;
+  int32_t heads;
+};
+
+static HeadGroup head_group(int32_t h0, int32_t heads, int32_t ws_slots, const void* q, int64_t q_stride_h, void* ws_o,
+                            float* ws_lse, void* out, int64_t out_stride_h, float* lse) {
+  HeadGroup g;
+  g.heads = heads - h0 < kHeadGroup ? heads - h0 : kHeadGroup;
+  g.q = q == nullptr ? nullptr : static_cast<const __bf16*>(q) + (int64_t)h0 * q_stride_h;
+  g.ws_o = ws_o == nullptr ? nullptr : static_cast<__bf16*>(ws_o) + (int64_t)ws_slots * h0 * MLA_V_DIM;
+  g.ws_lse = ws_lse == nullptr ? nullptr : ws_lse + (int64_t)ws_slots * h0;
+  g.out = static_cast<__bf16*>(out) + (int64_t)h0 * out_stride_h;
+  g.lse = lse == nullptr ? nullptr : lse + h0;
+  return g;
+}
+
+static int check_head_groups(const char* who, int32_t heads, int64_t q_stride_b, int64_t q_stride_h,
+                             int64_t out_stride_b, int64_t out_stride_h, const float* lse, int64_t lse_stride_b) {
+  if (heads < 1 || heads > kMaxHeads) return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be in [1, %d], got %d", who, kMaxHeads, heads);
+  if (q_stride_b < (int64_t)heads * q_stride_h || out_stride_b < (int64_t)heads * out_stride_h ||
+      (lse != nullptr && lse_stride_b < heads))
+    return fail(MLA_ERR_INVALID_ARG, "%s: batch strides of q / out / lse must hold %d heads", who, heads);
+  return MLA_OK;
+}
+
 int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                           int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                           int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
@@ -320,12 +356,18 @@ int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   const char* who = "mla_decode_split_bf16";
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
   if (batch == 0) return ok();
-  mla::DecodeParams p;
-  if (int rc = decode_params(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size, page_table,
-                             pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse, ws_slots, out,
-                             out_stride_b, out_stride_h, lse, lse_stride_b, &p))
+  if (int rc = check_head_groups(who, heads, q_stride_b, q_stride_h, out_stride_b, out_stride_h, lse, lse_stride_b))
     return rc;
-  return hip_status(mla::launch_decode(p, (hipStream_t)stream), "mla_decode_split_bf16 launch");
+  for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {
+    const HeadGroup g = head_group(h0, heads, ws_slots, q, q_stride_h, ws_o, ws_lse, out, out_stride_h, lse);
+    mla::DecodeParams p;
+    if (int rc = decode_params(who, g.q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size,
+                               page_table, pt_stride, seq_lens, batch, g.heads, scale, plan, num_ctas, g.ws_o,
+                               g.ws_lse, ws_slots, g.out, out_stride_b, out_stride_h, g.lse, lse_stride_b, &p))
+      return rc;
+    if (int rc = hip_status(mla::launch_decode(p, (hipStream_t)stream), "mla_decode_split_bf16 launch")) return rc;
+  }
+  return ok();
 }
 
 int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
@@ -337,16 +379,22 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
   const char* who = "mla_decode_bf16";
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
   if (batch == 0) return ok();
-  mla::DecodeParams p;
-  if (int rc = decode_params(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size, page_table,
-                             pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse, ws_slots, out,
-                             out_stride_b, out_stride_h, lse, lse_stride_b, &p))
+  if (int rc = check_head_groups(who, heads, q_stride_b, q_stride_h, out_stride_b, out_stride_h, lse, lse_stride_b))
     return rc;
-  hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
-  const mla::MergeParams m = merge_params(ws_o, ws_lse, ws_slots, plan + 4 * (int64_t)num_ctas, batch, heads, 1, out,
-                                          out_stride_b, out_stride_h, lse, lse_stride_b);
-  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch");
+  for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {
+    const HeadGroup g = head_group(h0, heads, ws_slots, q, q_stride_h, ws_o, ws_lse, out, out_stride_h, lse);
+    mla::DecodeParams p;
+    if (int rc = decode_params(who, g.q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size,
+                               page_table, pt_stride, seq_lens, batch, g.heads, scale, plan, num_ctas, g.ws_o,
+                               g.ws_lse, ws_slots, g.out, out_stride_b, out_stride_h, g.lse, lse_stride_b, &p))
+      return rc;
+    hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
+    const mla::MergeParams m = merge_params(g.ws_o, g.ws_lse, ws_slots, plan + 4 * (int64_t)num_ctas, batch, g.heads,
+                                            1, g.out, out_stride_b, out_stride_h, g.lse, lse_stride_b);
+    if (int rc = hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch")) return rc;
+  }
+  return ok();
 }
 
 int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
@@ -359,9 +407,15 @@ int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots
     return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
   if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
   if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
-  const mla::MergeParams m = merge_params(ws_o, ws_lse, ws_slots, req_info, batch, heads, single_piece_final ? 1 : 0,
-                                          out, out_stride_b, out_stride_h, lse, lse_stride_b);
-  return hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_merge_f32 launch");
+  for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {  // the workspace holds one [slots, group, 512] block per group
+    const HeadGroup g = head_group(h0, heads, ws_slots, nullptr, 0, const_cast<void*>(ws_o),
+                                   const_cast<float*>(ws_lse), out, out_stride_h, lse);
+    const mla::MergeParams m = merge_params(g.ws_o, g.ws_lse, ws_slots, req_info, batch, g.heads,
+                                            single_piece_final ? 1 : 0, g.out, out_stride_b, out_stride_h, g.lse,
+                                            lse_stride_b);
+    if (int rc = hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_merge_f32 launch")) return rc;
+  }
+  return ok();
 }
 
 int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_pool, int64_t k_row_stride,

@@ -70,10 +70,11 @@ def test_decode_heads_and_page_sizes(heads, ps):
     check_case(case, 64)
 
 
-@pytest.mark.parametrize("heads,ps", [(1, 64), (8, 64), (8, 16), (20, 32), (63, 128)])
+@pytest.mark.parametrize("heads,ps", [(1, 64), (8, 64), (8, 16), (20, 32), (63, 128), (128, 64), (96, 16)])
 def test_decode_tensor_parallel_head_counts(heads, ps):
     """Head counts that are not a multiple of 16 (a tensor-parallel shard: Kimi-K2 over 8 GPUs has
-    8 heads per GPU): the last wave's lanes without a head compute nothing that is stored."""
+    8 heads per GPU): the last wave's lanes without a head compute nothing that is stored. More
+    than 64 heads (DeepSeek-V3's 128 with attention data parallelism) run in groups of 64."""
     print(f"[decode heads] heads={heads} ps={ps}", flush=True)
     case = make_decode_case(6, heads, ps, lens=[1, 64, 65, 700, 2048, 33], seed=heads * 7 + ps)
     check_case(case, 64)
@@ -190,18 +191,21 @@ def test_page_table_kernel_bit_exact():
         assert torch.equal(got.cpu(), ref)
 
 
-def test_split_then_merge_equals_one_call():
-    """mla_decode_split_bf16 + mla_decode_merge_f32(single_piece_final) == mla_decode_bf16, bit for bit."""
-    case = make_decode_case(6, 64, 64, lens=[5000, 70, 1, 3000, 129, 640], seed=11)
+@pytest.mark.parametrize("heads", [64, 128, 80])
+def test_split_then_merge_equals_one_call(heads):
+    """mla_decode_split_bf16 + mla_decode_merge_f32(single_piece_final) == mla_decode_bf16, bit for bit
+    (more than 64 heads: groups of 64, each with its own block of the workspace)."""
+    print(f"[split+merge] heads={heads}", flush=True)
+    case = make_decode_case(6, heads, 64, lens=[5000, 70, 1, 3000, 129, 640], seed=11)
     q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
     plan_np, slots = lib.decode_plan(case.lens, 64, 32)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), 64, 512), dtype=torch.bfloat16, device=DEV)
-    ws_lse = torch.empty((max(slots, 1), 64), dtype=torch.float32, device=DEV)
+    ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.bfloat16, device=DEV)
+    ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
     outs = []
     for two_step in (False, True):
-        out = torch.empty((6, 64, 512), dtype=torch.bfloat16, device=DEV)
-        lse = torch.empty((6, 64), dtype=torch.float32, device=DEV)
+        out = torch.empty((6, heads, 512), dtype=torch.bfloat16, device=DEV)
+        lse = torch.empty((6, heads), dtype=torch.float32, device=DEV)
         lib.mla_decode(q, kv, pt, sl, plan, 32, ws_o, ws_lse, R.DEFAULT_SCALE, out, lse, split_only=two_step)
         if two_step:
             lib.mla_decode_merge(ws_o, ws_lse, plan[32 * 4 :], out, lse, single_piece_final=True)
@@ -209,6 +213,9 @@ def test_split_then_merge_equals_one_call():
         outs.append((out.cpu(), lse.cpu()))
     assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
     assert torch.equal(outs[0][1], outs[1][1])
+    o_ref, lse_ref = R.mla_decode(case.q, case.kv_pool, case.page_table, case.lens)
+    torch.testing.assert_close(outs[0][0].float(), o_ref, **O_TOL)
+    torch.testing.assert_close(outs[0][1], lse_ref, **LSE_TOL)
 
 
 def test_decode_long_context_split_kv():

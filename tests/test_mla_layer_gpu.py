@@ -85,6 +85,13 @@ def test_mla_layer_kimi_k2_tp8_shard():
     _run_case(H=8, hidden=7168, q_lora=1536, steps=steps, seed=2)
 
 
+def test_mla_layer_deepseek_v3_shape():
+    """DeepSeek-V3 attention with data-parallel attention: all 128 heads on one GPU (decode runs
+    two 64-head groups), hidden 7168, q_lora 1536."""
+    steps = [("prefill", {0: 100, 1: 45}), ("decode", {0: 1, 1: 1}), ("prefill", {1: 30}), ("decode", {0: 1, 1: 1})]
+    _run_case(H=128, hidden=7168, q_lora=1536, steps=steps, seed=4)
+
+
 def test_mla_layer_decode_graph_replay():
     """A decode layer step captured in a HIP graph and replayed (with eager work between replays)
     gives the eager step's output every time."""
