@@ -171,6 +171,7 @@ class MLAAttentionLayer:
     def __init__(self, layer_id: int, cfg: MLALayerConfig, weights: MLAWeights, ops=None) -> None:
         a = cfg.attn
         assert a.kv_lora_rank == 512 and a.qk_rope_head_dim == 64, "the HIP kernels take 512 + 64 latent rows"
+        assert cfg.q_lora_rank % 8 == 0, "the latent part of the fused q_a / kv_a output must stay 16-byte aligned"
         assert abs(a.softmax_mscale - softmax_mscale(cfg.rope_scaling)) < 1e-12, (
             "MLAConfig.softmax_mscale must be softmax_mscale(rope_scaling): the backend's scale comes from it"
         )
@@ -183,6 +184,8 @@ class MLAAttentionLayer:
             device
         )
         # absorption matrices, contiguous per head (batched products take no transposed views)
+        # q_a and kv_a read the same input: one GEMM over their stacked rows [q_lora + 576, hidden]
+        self.w_qkv_a = torch.cat((weights.q_a, weights.kv_a), dim=0).contiguous()
         self.w_uk = weights.w_uk(a).contiguous()  # [H, 128, 512]
         self.w_uv_t = weights.w_uv(a).transpose(1, 2).contiguous()  # [H, 512, 128]
         self.w_uk_flat = self.w_uk.reshape(-1, a.kv_lora_rank)  # [H*128, 512]
@@ -207,8 +210,10 @@ class MLAAttentionLayer:
         ops, eps, inter = self.ops, self.cfg.rms_eps, self.cfg.rope_interleaved
         pos = batch.positions.to(torch.int32)  # no copy when the scheduler already gives int32
 
-        q = (ops.rms_norm(x @ self.w.q_a.t(), self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
-        latent = ops.latent_rows(x @ self.w.kv_a.t(), self.w.kv_a_norm, pos, self.cos_sin, eps, inter)  # [T, 576]
+        qkv_a = x @ self.w_qkv_a.t()  # [T, q_lora + 576]
+        r = self.cfg.q_lora_rank
+        q = (ops.rms_norm(qkv_a[:, :r], self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
+        latent = ops.latent_rows(qkv_a[:, r:], self.w.kv_a_norm, pos, self.cos_sin, eps, inter)  # [T, 576]
 
         if batch.is_decode:
             # absorbed: q_abs = [q_nope W_UK | rope(q_pe)] per head; the nope dims go head-major for the bmm
