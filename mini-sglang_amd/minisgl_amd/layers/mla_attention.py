@@ -220,12 +220,15 @@ class MLAAttentionLayer:
             q_abs = torch.empty((T, H, a.kv_dim), dtype=x.dtype, device=x.device)
             q_nope_h = torch.empty((H, T, a.qk_nope_head_dim), dtype=x.dtype, device=x.device)
             ops.q_rope(q, pos, self.cos_sin, inter, q_abs[..., a.kv_lora_rank :], q_nope_h.transpose(0, 1))
-            q_abs[..., : a.kv_lora_rank] = torch.bmm(q_nope_h, self.w_uk).transpose(0, 1)
+            # the bmm writes each head's q_nope W_UK straight into the absorbed query's first 512 dims
+            torch.bmm(q_nope_h, self.w_uk, out=q_abs[..., : a.kv_lora_rank].transpose(0, 1))
             if pool.has_prefill_pages:  # keep the per-head pages whole for a later prefill over this prefix
                 k, v = self._decompress(latent)
                 pool.store_kv(k, v, batch.out_loc, self.layer_id)
             o_lat = backend.forward(q_abs, latent, None, self.layer_id, batch)  # stores the latent rows
-            o = torch.bmm(o_lat.transpose(0, 1).contiguous(), self.w_uv_t).transpose(0, 1)  # [T, H, 128]
+            # o[t, h] = o_lat[t, h] W_UV[h]^T, read and written through head-major views (no copies)
+            o = torch.empty((T, H, a.v_head_dim), dtype=x.dtype, device=x.device)
+            torch.bmm(o_lat.transpose(0, 1), self.w_uv_t, out=o.transpose(0, 1))
         else:
             pool.store_kv(latent, None, batch.out_loc, self.layer_id)  # for the decode steps to come
             ops.q_rope(q, pos, self.cos_sin, inter, q[..., a.qk_nope_head_dim :])  # in place
