@@ -8,6 +8,7 @@ import torch
 from ..config import MLAConfig
 from .base import BaseKVCachePool
 from .mla_pool import MLAKVCache
+from .page_table import PagedTokenTable
 
 
 def create_kvcache_pool(
@@ -32,4 +33,4 @@ def create_kvcache_pool(
     )
 
 
-__all__ = ["BaseKVCachePool", "MLAKVCache", "create_kvcache_pool"]
+__all__ = ["BaseKVCachePool", "MLAKVCache", "PagedTokenTable", "create_kvcache_pool"]

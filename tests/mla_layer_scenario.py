@@ -63,7 +63,9 @@ def scaled_steps(factor: int) -> List[Tuple[str, Dict[int, int]]]:
 
 def total_lens(steps) -> Dict[int, int]:
     tot: Dict[int, int] = {}
-    for _, st in steps:
+    for ph, st in steps:
+        if ph == "free":
+            continue
         for r, e in st.items():
             tot[r] = tot.get(r, 0) + e
     return tot
@@ -83,17 +85,27 @@ def token_table(lens: Dict[int, int], page_size: int, gen: torch.Generator, spar
     return tt, num_pages
 
 
-def run(layer, ctx, backend, x_hist: Dict[int, torch.Tensor], steps, tt: torch.Tensor, device):
+def run(layer, ctx, backend, x_hist: Dict[int, torch.Tensor], steps, tt: torch.Tensor, device, alloc=None):
     """Run ``steps`` through ``layer``; yields (phase, [(request, new tokens)], tokens per request
-    after the step, output [T, hidden])."""
+    after the step, output [T, hidden]). With ``alloc`` (a PagedTokenTable over ``ctx.page_table``)
+    pages are allocated step by step as the scheduler does, and a ("free", {r: 0}) step returns a
+    finished request's pages."""
     cached = {r: 0 for r in x_hist}
     for phase, st in steps:
+        if phase == "free":
+            for r in st:
+                alloc.free(r, cached[r])
+            continue
         order = sorted(st)
         reqs = [Req(table_idx=r, cached_len=cached[r], device_len=cached[r] + st[r]) for r in order]
         batch = Batch(reqs=reqs, phase=phase)
         batch.padded_reqs = reqs
         batch.positions = torch.cat([torch.arange(q.cached_len, q.device_len) for q in reqs]).to(torch.int32).to(device)
-        batch.out_loc = torch.cat([tt[q.table_idx, q.cached_len : q.device_len] for q in reqs]).to(device)
+        if alloc is not None:
+            alloc.allocate_paged(reqs)
+            batch.out_loc = alloc.out_loc(reqs)
+        else:
+            batch.out_loc = torch.cat([tt[q.table_idx, q.cached_len : q.device_len] for q in reqs]).to(device)
         x = torch.cat([x_hist[r][cached[r] : cached[r] + st[r]] for r in order]).to(device)
         backend.prepare_metadata(batch)
         with ctx.forward_batch(batch):

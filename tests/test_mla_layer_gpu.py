@@ -92,6 +92,47 @@ def test_mla_layer_deepseek_v3_shape():
     _run_case(H=128, hidden=7168, q_lora=1536, steps=steps, seed=4)
 
 
+def test_mla_layer_with_page_allocator():
+    """Pages allocated step by step by the token-table writer (as the scheduler does), a finished
+    request's pages freed and reused by a new request, so rows hold non-contiguous pages."""
+    from minisgl_amd.kvcache import PagedTokenTable
+
+    reset_global_ctx()
+    gen = torch.Generator().manual_seed(6)
+    H, hidden, ps = 16, 1024, 64
+    attn = MLAConfig(num_heads=H, num_layers=1, softmax_mscale=softmax_mscale(KIMI_YARN))
+    cfg = MLALayerConfig(attn=attn, hidden_size=hidden, q_lora_rank=384, rope_theta=50000.0, max_position=16384,
+                         rope_scaling=KIMI_YARN)
+    weights = MLAWeights.random(cfg, gen, DEV)
+    steps = [("prefill", {0: 150, 1: 90}), ("decode", {0: 1, 1: 1}), ("free", {1: 0}),
+             ("prefill", {2: 300}), ("decode", {0: 1, 2: 1}), ("prefill", {0: 70}), ("decode", {0: 1, 2: 1})]
+    lens = S.total_lens(steps)
+    num_pages = 12
+    ctx = Context(page_size=ps)
+    set_global_ctx(ctx)
+    ctx.page_table = torch.zeros((4, 512), dtype=torch.int32, device=DEV)
+    alloc = PagedTokenTable(num_pages, ps, ctx.page_table)
+    alloc.free_slots = alloc.free_slots[torch.randperm(num_pages, generator=gen).to(DEV)]  # a long-running server's order
+    ctx.kv_cache = create_kvcache_pool(attn, num_pages, ps, torch.bfloat16, DEV, with_prefill_pages=True)
+    backend = create_attention_backend("mla", attn)
+    ctx.attn_backend = backend
+    layer = MLAAttentionLayer(0, cfg, weights)
+    x_hist = {r: torch.randn((L, hidden), generator=gen).to(torch.bfloat16) for r, L in lens.items()}
+    Wd = {k: getattr(weights, k).cpu().double() for k in WEIGHT_NAMES}
+    kw = dict(num_heads=H, rope_dim=64, rope_theta=50000.0, rope_scaling=dict(KIMI_YARN), interleaved=True,
+              scale=attn.softmax_scale, round_bf16=True)
+    try:
+        for phase, new, after, out in S.run(layer, ctx, backend, x_hist, steps, None, DEV, alloc=alloc):
+            torch.cuda.synchronize()
+            want = S.expected({r: x.double() for r, x in x_hist.items()}, new, after, Wd, **kw)
+            rel = float((out.double().cpu() - want).norm() / want.norm())
+            print(f"[mla layer alloc] {phase} {new}: rel err {rel:.2e}, free pages {alloc.free_pages}", flush=True)
+            torch.testing.assert_close(out.double().cpu(), want, atol=2e-2, rtol=2e-2)
+            assert rel < 1e-2
+    finally:
+        reset_global_ctx()
+
+
 def test_mla_layer_decode_graph_replay():
     """A decode layer step captured in a HIP graph and replayed (with eager work between replays)
     gives the eager step's output every time."""
