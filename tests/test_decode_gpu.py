@@ -96,6 +96,27 @@ def test_decode_tensor_parallel_head_counts(heads, ps):
     torch.testing.assert_close(wide_lse[:, :heads].cpu(), lse_ref, **LSE_TOL)
 
 
+@pytest.mark.parametrize("num_ctas", [256, 8])
+def test_decode_many_short_requests(num_ctas):
+    """1024 requests of 0..200 tokens: at 8 CTAs each CTA's range holds the plan's maximum of 128
+    requests (the streaming kernel stages per-request bounds in LDS)."""
+    print(f"[decode many] num_ctas={num_ctas}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    lens = torch.randint(0, 201, (1024,), generator=g).tolist()
+    case = make_decode_case(1024, 64, 64, lens=lens, seed=21)
+    plan_np, _ = lib.decode_plan(lens, 64, num_ctas)
+    cta = plan_np[: num_ctas * lib.PLAN_CTA_INTS].reshape(num_ctas, 4)
+    per_cta = [min(int(re_) if ke == 0 else int(re_) + 1, 1024) - int(rb) for rb, _, re_, ke in cta]
+    assert max(per_cta) <= lib.MAX_CTA_REQUESTS
+    check_case(case, num_ctas)
+
+
+def test_decode_one_long_request_over_every_cta():
+    """One 131072-token request split over all 256 CTAs: the merge reads 256 pieces per head."""
+    case = make_decode_case(1, 64, 64, lens=[131072], seed=22)
+    check_case(case, 256)
+
+
 def test_decode_long_split_merge():
     """Long requests split over many CTAs exercise the LSE merge kernel."""
     case = make_decode_case(3, 64, 64, lens=[20000, 4097, 130], seed=3)
