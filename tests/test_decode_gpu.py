@@ -111,6 +111,16 @@ def test_decode_many_short_requests(num_ctas):
     check_case(case, num_ctas)
 
 
+def test_decode_kimi_k2_full_batch():
+    """The benchmark's batch at full size: B=64, H=64, lengths U[1024, 8192], page 64, random pages."""
+    case = make_decode_case(64, 64, 64, len_range=(1024, 8192), device=DEV, seed=0)
+    out, lse, slots = run_decode(case.q, case.kv_pool, case.page_table, case.seq_lens, case.lens, 64, 256)
+    assert slots > 0
+    o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
+    torch.testing.assert_close(out, o_ref, **O_TOL)
+    torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
+
+
 def test_decode_one_long_request_over_every_cta():
     """One 131072-token request split over all 256 CTAs: the merge reads 256 pieces per head."""
     case = make_decode_case(1, 64, 64, lens=[131072], seed=22)

@@ -125,3 +125,51 @@ def test_prefill_single_dominant_key():
     _set_key_dim0(case, lambda t, L: torch.where(t == 517, 240.0, 0.0))
     case.q[..., 0] = 8.0
     check_case(case)
+
+
+def test_prefill_full_bench_batch_sampled_rows_and_chunking():
+    """The benchmark's batch at full size (B=4, H=64, E=2048, P~U[0,8192], page 64): sampled query
+    rows of every request against the oracle, and chunk invariance: the same requests prefilled as
+    two 1024-row chunks (the first over keys up to P + 1024, the second over the whole prefix)
+    give the full run's rows bit for bit."""
+    g = torch.Generator().manual_seed(0)
+    prefixes = torch.randint(0, 8193, (4,), generator=g).tolist()
+    print(f"[prefill full] prefixes={prefixes}", flush=True)
+    E, H, ps = 2048, 64, 64
+    case = make_prefill_case(H, ps, extends=[E] * 4, prefixes=prefixes, device=DEV, seed=0)
+    T = 4 * E
+
+    def run(q, cu, lens):
+        out = torch.full((q.shape[0], H, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+        lse = torch.full((q.shape[0], H), float("nan"), dtype=torch.float32, device=DEV)
+        lib.mla_prefill(q, case.k_pool, case.v_pool, case.page_table, cu, lens, R.DEFAULT_SCALE, out, lse)
+        torch.cuda.synchronize()
+        return out, lse
+
+    out, lse = run(case.q, case.cu_seqlens_q, case.seq_lens_k)
+    # chunk invariance
+    half = E // 2
+    cu_half = torch.arange(0, T // 2 + 1, half, dtype=torch.int32, device=DEV)
+    first = torch.cat([torch.arange(b * E, b * E + half) for b in range(4)]).to(DEV)
+    second = first + half
+    lens_first = torch.tensor([P + half for P in prefixes], dtype=torch.int32, device=DEV)
+    o1, l1 = run(case.q[first].contiguous(), cu_half, lens_first)
+    o2, l2 = run(case.q[second].contiguous(), cu_half, case.seq_lens_k)
+    assert torch.equal(o1.view(torch.int16), out[first].view(torch.int16)) and torch.equal(l1, lse[first])
+    assert torch.equal(o2.view(torch.int16), out[second].view(torch.int16)) and torch.equal(l2, lse[second])
+    # sampled rows against the oracle: block edges, the diagonal's ends, and random rows
+    kflat = case.k_pool.reshape(-1, H, 192)
+    vflat = case.v_pool.reshape(-1, H, 128)
+    gen = torch.Generator().manual_seed(1)
+    for b, P in enumerate(prefixes):
+        L = P + E
+        rows = R.token_rows(case.page_table[b].cpu(), L, ps).to(DEV)
+        k = kflat[rows].float().cpu().transpose(0, 1)
+        v = vflat[rows].float().cpu().transpose(0, 1)
+        pick = torch.cat((torch.tensor([0, 1, 31, 32, 255, 256, 1023, 1024, E - 2, E - 1]),
+                          torch.randint(0, E, (22,), generator=gen))).unique()
+        qs = case.q[b * E + pick.to(DEV)].float().cpu().transpose(0, 1)
+        mask = torch.arange(L)[None, :] <= (P + pick)[:, None]
+        o_ref, lse_ref = R._attend(qs, k, v, R.DEFAULT_SCALE, mask[None])
+        torch.testing.assert_close(out[b * E + pick.to(DEV)].float().cpu(), o_ref.transpose(0, 1), **O_TOL)
+        torch.testing.assert_close(lse[b * E + pick.to(DEV)].cpu(), lse_ref.transpose(0, 1), **LSE_TOL)
