@@ -9,15 +9,17 @@
 //    piece boundaries, queries included, so a new piece never drains it. The
 //    page id of every KV tile and the bounds of every request of the range
 //    are staged in LDS once, at CTA start.
-//  * 4 waves = 2 head groups (32 heads each) x 2 halves. Wave (hg, th):
+//  * 4 waves = 2 head groups (32 heads each) x 2 halves for the scores, and
+//    4 quarters of the value dims for the output. Wave w = (hg, th):
 //      S^T[16 tokens (half th) x 32 heads] = K . Q^T     36 MFMAs, 18 K reads
-//      softmax numerators of those 16 tokens, exchanged with the partner
-//      wave (hg, 1 - th) as bf16 through LDS
-//      O^T[256 dims (half th) x 32 heads] += V^T . P^T   32 MFMAs, 32 V reads
-//    over all 32 tokens. Every staged K row is read by 2 waves and every V
-//    row half by 2 waves, and no MFMA or exponential is computed twice. The
-//    pair agrees on the exponent reference at the first tile of each piece
-//    and adds its row sums at the end of the piece.
+//      softmax numerators of those 16 tokens, published as bf16 through LDS
+//      so that every wave holds P for all 64 heads and 32 tokens
+//      O^T[128 dims (quarter w) x 64 heads] += V^T . P^T 32 MFMAs, 16 V reads
+//    Every staged K row is read by 2 waves and every V row by 1 wave, and no
+//    MFMA or exponential is computed twice. The pair (hg, 0) / (hg, 1) agrees
+//    on the exponent reference at the first tile of each piece; at its end the
+//    row sums and references of all heads are exchanged, since every wave
+//    normalises and writes its dims of all 64 heads.
 //  * Barriers wait on LDS only, so the vector-memory operations in flight are
 //    the ring's DMA loads and the output stores, both counted explicitly.
 #include "mla_common.h"
@@ -43,6 +45,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   // pair exchange: softmax numerators (16 B per lane), per-head maxima and row sums
   __shared__ __attribute__((aligned(16))) u32x4 s_xp[kSWaves][64];
   __shared__ float s_xm[kSWaves][32];
+  __shared__ float s_xr[kSWaves][32];  // per-head exponent references, for the waves that finalise other heads
   __shared__ int s_flag[kSWaves];
   // the CTA's range, staged once: per request r (= b - rb) its piece [t0, t1),
   // first stream tile, pieces and partial-slot offset; per stream tile its page id
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   int v_off[4];  // this wave's value half starts 512 bytes into the row (before swizzle groups)
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
-    v_off[q4] = (4 * g + (c >> 2)) * kRowBytes + 512 * th +
+    v_off[q4] = (4 * g + (c >> 2)) * kRowBytes + 256 * wave +
                 ((2 * (q4 ^ (c >> 2)) + (((c & 3) >> 1) ^ (g & 1))) << 4) + ((c & 1) << 3);
   uint32_t dma_voff[kSDma];
 #pragma unroll
@@ -223,7 +226,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
   prologue();
 
   // ---- piece state; m_max and overflow are tracked per lane and reduced when needed
-  f32x4 O[2][16];
+  f32x4 O[4][8];  // O^T of head block 0..3 (16 heads each), this wave's 8 dim blocks
   float m_ref[2] = {0.f, 0.f}, m_max[2], l_run[2];
   bool overflow = false;
   int attempt = 0;
@@ -280,9 +283,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     }
     if (piece_start) {
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
+      for (int hq = 0; hq < 4; ++hq) {
 #pragma unroll
-        for (int db = 0; db < 16; ++db) O[hb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < 8; ++db) O[hq][db] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
       l_run[0] = l_run[1] = 0.f;
       m_max[0] = m_max[1] = -INFINITY;
@@ -362,27 +365,28 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
     // P^T B operand of lane (g, c): k = 8g + i is token 4g + i (i < 4, half 0) or 16 + 4g + i - 4 (half 1)
     s_xp[wave][lane] = u32x4{pown[0][0], pown[0][1], pown[1][0], pown[1][1]};
     barrier_lds();
-    const u32x4 pp = s_xp[partner][lane];
-    bf16x8 pb[2];
-    if (th == 0) {
-      pb[0] = __builtin_bit_cast(bf16x8, (u32x4{pown[0][0], pown[0][1], pp[0], pp[1]}));
-      pb[1] = __builtin_bit_cast(bf16x8, (u32x4{pown[1][0], pown[1][1], pp[2], pp[3]}));
-    } else {
-      pb[0] = __builtin_bit_cast(bf16x8, (u32x4{pp[0], pp[1], pown[0][0], pown[0][1]}));
-      pb[1] = __builtin_bit_cast(bf16x8, (u32x4{pp[2], pp[3], pown[1][0], pown[1][1]}));
+    // P^T B operands of all 64 heads: head block 2 hg' + hb takes tokens 0..15 from wave hg' and
+    // tokens 16..31 from wave hg' + 2
+    bf16x8 pb[4];
+#pragma unroll
+    for (int hgi = 0; hgi < 2; ++hgi) {
+      const u32x4 p0 = s_xp[hgi][lane], p1 = s_xp[hgi + 2][lane];
+      pb[2 * hgi + 0] = __builtin_bit_cast(bf16x8, (u32x4{p0[0], p0[1], p1[0], p1[1]}));
+      pb[2 * hgi + 1] = __builtin_bit_cast(bf16x8, (u32x4{p0[2], p0[3], p1[2], p1[3]}));
     }
 
-    // ---- O^T[16 dims x 16 heads] += V^T . P^T: this wave's 16 dim blocks, both head blocks
+    // ---- O^T[16 dims x 16 heads] += V^T . P^T: this wave's 8 dim blocks, all 4 head blocks (every
+    // staged V row is read by one wave)
 #pragma unroll
-    for (int db = 0; db < 16; ++db) {
+    for (int db = 0; db < 8; ++db) {
       const bf16x8 a =
           __builtin_shufflevector(vlo[db % kSVPrefetch], vhi[db % kSVPrefetch], 0, 1, 2, 3, 4, 5, 6, 7);
-      if (db + kSVPrefetch < 16) {
+      if (db + kSVPrefetch < 8) {
         vlo[db % kSVPrefetch] = vread(db + kSVPrefetch, 0);
         vhi[db % kSVPrefetch] = vread(db + kSVPrefetch, 1);
       }
-      O[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0], O[0][db], 0, 0, 0);
-      O[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1], O[1][db], 0, 0, 0);
+#pragma unroll
+      for (int hq = 0; hq < 4; ++hq) O[hq][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[hq], O[hq][db], 0, 0, 0);
     }
 
     const bool piece_end = comp.t + kTile >= comp.t1;
@@ -393,6 +397,8 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
       if (g == 0) {
         s_xm[wave][c] = lw0;
         s_xm[wave][16 + c] = lw1;
+        s_xr[wave][c] = m_ref[0];
+        s_xr[wave][16 + c] = m_ref[1];
       }
       const bool wave_overflow = __ballot(overflow) != 0;
       if (lane == 0) s_flag[wave] = wave_overflow ? 1 : 0;
@@ -424,45 +430,54 @@ __global__ __launch_bounds__(256, 1) void mla_decode_stream_kernel(const DecodeP
         continue;
       }
       attempt = 0;
-      const float l_tot[2] = {lw0 + s_xm[partner][c], lw1 + s_xm[partner][16 + c]};
+      // every wave holds all 64 heads' outputs for its dims: row sums (both token halves) and
+      // exponent references of head block 2 hg' + hb come from waves hg' and hg' + 2
+      float l_tot[4], m_all[4];
+#pragma unroll
+      for (int hq = 0; hq < 4; ++hq) {
+        const int src = hq >> 1, hx = 16 * (hq & 1) + c;
+        l_tot[hq] = s_xm[src][hx] + s_xm[src + 2][hx];
+        m_all[hq] = s_xr[src][hx];
+      }
 
-      // ---- finalise: lane holds heads 32hg+16hb+c, dims 256th + 16db + 4g + (0..3)
+      // ---- finalise: lane holds heads 16hq+c, dims 128wave + 16db + 4g + (0..3); wave w writes the
+      // LSE of head block w
       const int b = rb + comp.r;
       const int npieces = __builtin_amdgcn_readfirstlane(s_np[comp.r]);
       int stores = 0;
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        const int h = 32 * hg + 16 * hb + c;
-        const float inv = l_tot[hb] > 0.f ? 1.f / l_tot[hb] : 0.f;
+      for (int hq = 0; hq < 4; ++hq) {
+        const int h = 16 * hq + c;
+        const float inv = l_tot[hq] > 0.f ? 1.f / l_tot[hq] : 0.f;
         const float lse_nat =
-            l_tot[hb] > 0.f ? (m_ref[hb] + log2f(l_tot[hb])) * 0.69314718055994531f : -INFINITY;
+            l_tot[hq] > 0.f ? (m_all[hq] + log2f(l_tot[hq])) * 0.69314718055994531f : -INFINITY;
         if (npieces == 1) {
-          __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 256 * th + 4 * g;
+          __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 128 * wave + 4 * g;
 #pragma unroll
-          for (int db = 0; db < 16; ++db) {
+          for (int db = 0; db < 8; ++db) {
             u32x2 v;
-            v[0] = pack_bf16x2(O[hb][db][0] * inv, O[hb][db][1] * inv);
-            v[1] = pack_bf16x2(O[hb][db][2] * inv, O[hb][db][3] * inv);
+            v[0] = pack_bf16x2(O[hq][db][0] * inv, O[hq][db][1] * inv);
+            v[1] = pack_bf16x2(O[hq][db][2] * inv, O[hq][db][3] * inv);
             *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
           }
-          stores += 16;
-          if (p.lse != nullptr && th == 0) {
+          stores += 8;
+          if (p.lse != nullptr && hq == wave) {
             if (g == 0) p.lse[(int64_t)b * p.lse_stride_b + h] = lse_nat;
             stores += 1;
           }
         } else {
           const int slot = __builtin_amdgcn_readfirstlane(s_slot0[comp.r]) + w;
           if (slot >= 0 && slot < p.ws_slots) {
-            __bf16* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 256 * th + 4 * g;
+            __bf16* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 128 * wave + 4 * g;
 #pragma unroll
-            for (int db = 0; db < 16; ++db) {
+            for (int db = 0; db < 8; ++db) {
               u32x2 v;
-              v[0] = pack_bf16x2(O[hb][db][0] * inv, O[hb][db][1] * inv);
-              v[1] = pack_bf16x2(O[hb][db][2] * inv, O[hb][db][3] * inv);
+              v[0] = pack_bf16x2(O[hq][db][0] * inv, O[hq][db][1] * inv);
+              v[1] = pack_bf16x2(O[hq][db][2] * inv, O[hq][db][3] * inv);
               *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
             }
-            stores += 16;
-            if (th == 0) {
+            stores += 8;
+            if (hq == wave) {
               if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
               stores += 1;
             }
