@@ -211,6 +211,17 @@ int mla_latent_rows_bf16(const void *kv, int64_t kv_row_stride, const void *norm
                          void *stream);
 
 /*
+ * mla_qkv_a_rows_bf16: both halves of the fused q_a / kv_a projection output in one launch,
+ * qkv [rows, q_rank + 576] (row stride qkv_row_stride): qkv[r][0:q_rank] is normalised in place
+ * (RMSNorm with q_norm_weight), and latent_out[r] = the latent row of qkv[r][q_rank:] as
+ * mla_latent_rows_bf16 computes it. q_rank a multiple of 8.
+ */
+int mla_qkv_a_rows_bf16(void *qkv, int64_t qkv_row_stride, int32_t q_rank, const void *q_norm_weight,
+                        const void *kv_norm_weight, const int32_t *positions, const float *cos_sin,
+                        int32_t max_position, int32_t rows, float eps, int32_t interleaved, void *latent_out,
+                        int64_t latent_row_stride, void *stream);
+
+/*
  * mla_q_rope_bf16: queries q [tokens, heads, 192] (128 nope + 64 rope dims, strides
  * (q_stride_t, q_stride_h)): pe_out[t, h, 0:64] = RoPE of q[t, h, 128:192] at positions[t]
  * (pe_out may be q + 128 with q's strides: in place); if nope_out is not NULL,

@@ -505,6 +505,28 @@ int mla_latent_rows_bf16(const void* kv, int64_t kv_row_stride, const void* norm
                     "mla_latent_rows_bf16 launch");
 }
 
+int mla_qkv_a_rows_bf16(void* qkv, int64_t qkv_row_stride, int32_t q_rank, const void* q_norm_weight,
+                        const void* kv_norm_weight, const int32_t* positions, const float* cos_sin,
+                        int32_t max_position, int32_t rows, float eps, int32_t interleaved, void* latent_out,
+                        int64_t latent_row_stride, void* stream) {
+  const char* who = "mla_qkv_a_rows_bf16";
+  if (rows < 0 || max_position <= 0 || q_rank <= 0 || q_rank % 8 != 0)
+    return fail(MLA_ERR_INVALID_ARG, "%s: rows %d, max_position %d, q_rank %d (a positive multiple of 8)", who, rows,
+                max_position, q_rank);
+  if (rows == 0) return ok();
+  if (qkv == nullptr || q_norm_weight == nullptr || kv_norm_weight == nullptr || positions == nullptr ||
+      cos_sin == nullptr || latent_out == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!rows_ok(qkv, qkv_row_stride, (int64_t)q_rank + mla::kKvDim) || !rows_ok(latent_out, latent_row_stride, mla::kKvDim) ||
+      !aligned(q_norm_weight, 16) || !aligned(kv_norm_weight, 16))
+    return fail(MLA_ERR_INVALID_ARG, "%s: rows must be 16-byte aligned with strides multiples of 8 holding q_rank + 576",
+                who);
+  return hip_status(mla::launch_qkv_a_rows(qkv, qkv_row_stride, q_rank, q_norm_weight, kv_norm_weight, positions,
+                                           cos_sin, max_position, latent_out, latent_row_stride, rows, eps, interleaved,
+                                           (hipStream_t)stream),
+                    "mla_qkv_a_rows_bf16 launch");
+}
+
 int mla_q_rope_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, int32_t tokens, int32_t heads,
                     const int32_t* positions, const float* cos_sin, int32_t max_position, int32_t interleaved,
                     void* pe_out, int64_t pe_stride_t, int64_t pe_stride_h, void* nope_out, int64_t nope_stride_t,

@@ -111,6 +111,9 @@ hipError_t launch_rmsnorm(const void* x, int64_t xs, const void* w, void* out, i
 hipError_t launch_latent_rows(const void* kv, int64_t kvs, const void* w, const int32_t* pos, const float* cos_sin,
                               int32_t max_pos, void* out, int64_t os, int32_t rows, float eps, int32_t interleaved,
                               hipStream_t stream);
+hipError_t launch_qkv_a_rows(void* qkv, int64_t qkvs, int32_t q_rank, const void* q_w, const void* kv_w,
+                             const int32_t* pos, const float* cos_sin, int32_t max_pos, void* out, int64_t os,
+                             int32_t rows, float eps, int32_t interleaved, hipStream_t stream);
 hipError_t launch_q_rope(const void* q, int64_t qst, int64_t qsh, int32_t tokens, int32_t heads, const int32_t* pos,
                          const float* cos_sin, int32_t max_pos, int32_t interleaved, void* pe, int64_t pst, int64_t psh,
                          void* nope, int64_t nst, int64_t nsh, hipStream_t stream);

@@ -108,6 +108,56 @@ __global__ __launch_bounds__(256) void latent_rows_kernel(const __bf16* __restri
   }
 }
 
+// The q_a / kv_a projection's rows, fused: qkv[r] = [q_a (q_rank) | kv (576)]. One wave per token
+// normalises the q_a part in place (RMSNorm with q_w) and writes the token's latent row (RMSNorm
+// of the kv part's 512 latent dims with kv_w, RoPE of its 64 rope dims) to out[r].
+__global__ __launch_bounds__(256) void qkv_a_rows_kernel(__bf16* qkv, int64_t qkvs, int q_rank,
+                                                         const __bf16* __restrict__ q_w,
+                                                         const __bf16* __restrict__ kv_w,
+                                                         const int32_t* __restrict__ pos,
+                                                         const float* __restrict__ cos_sin, int max_pos,
+                                                         __bf16* __restrict__ out, int64_t os, int rows, float eps,
+                                                         int interleaved) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  __bf16* qr = qkv + (int64_t)row * qkvs;
+  // q_a part: sum of squares, then scale in place (each lane rereads only its own chunks)
+  float ss = 0.f;
+  for (int c = lane * 8; c < q_rank; c += 512) {
+    float f[8];
+    unpack8(*reinterpret_cast<const u32x4*>(qr + c), f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss += f[k] * f[k];
+  }
+  const float qinv = rsqrtf(wave_sum64(ss) / (float)q_rank + eps);
+  for (int c = lane * 8; c < q_rank; c += 512) {
+    float f[8], g[8];
+    unpack8(*reinterpret_cast<const u32x4*>(qr + c), f);
+    unpack8(*reinterpret_cast<const u32x4*>(q_w + c), g);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = f[k] * qinv * g[k];
+    *reinterpret_cast<u32x4*>(qr + c) = pack8(f);
+  }
+  // kv part: the latent row
+  const __bf16* r = qr + q_rank;
+  __bf16* orow = out + (int64_t)row * os;
+  float f[8], g[8];
+  unpack8(*reinterpret_cast<const u32x4*>(r + 8 * lane), f);
+  float s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s2 += f[k] * f[k];
+  const float inv = rsqrtf(wave_sum64(s2) / (float)kVDim + eps);
+  unpack8(*reinterpret_cast<const u32x4*>(kv_w + 8 * lane), g);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) f[k] = f[k] * inv * g[k];
+  *reinterpret_cast<u32x4*>(orow + 8 * lane) = pack8(f);
+  if (lane < kRopeDim / 2) {
+    const int p = min(max(pos[row], 0), max_pos - 1);
+    rope_pair(r + kVDim, orow + kVDim, lane, cos_sin + (int64_t)p * kRopeDim, interleaved);
+  }
+}
+
 // Query (t, h) = q[t, h, 0:192] (128 nope + 64 rope dims): pe_out[t, h, 0:64] = RoPE of the rope
 // dims at positions[t]; if nope_out is given, nope_out[t, h, 0:128] (own strides, e.g. head-major)
 // = the nope dims. pe_out may alias the rope dims of q (in place). One wave per (t, h).
@@ -147,6 +197,16 @@ hipError_t launch_latent_rows(const void* kv, int64_t kvs, const void* w, const 
   if (rows == 0) return hipSuccess;
   hipLaunchKernelGGL(latent_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, (const __bf16*)kv, kvs,
                      (const __bf16*)w, pos, cos_sin, max_pos, (__bf16*)out, os, rows, eps, interleaved);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_a_rows(void* qkv, int64_t qkvs, int32_t q_rank, const void* q_w, const void* kv_w,
+                             const int32_t* pos, const float* cos_sin, int32_t max_pos, void* out, int64_t os,
+                             int32_t rows, float eps, int32_t interleaved, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(qkv_a_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, (__bf16*)qkv, qkvs, q_rank,
+                     (const __bf16*)q_w, (const __bf16*)kv_w, pos, cos_sin, max_pos, (__bf16*)out, os, rows, eps,
+                     interleaved);
   return hipGetLastError();
 }
 

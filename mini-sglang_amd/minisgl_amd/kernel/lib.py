@@ -55,6 +55,9 @@ SIGNATURES = {
     "mla_latent_rows_bf16": (
         ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _i32, _vp, _i64, _vp]
     ),
+    "mla_qkv_a_rows_bf16": (
+        ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _i32, _vp, _i64, _vp]
+    ),
     "mla_q_rope_bf16": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp],
@@ -323,3 +326,30 @@ def q_rope(q, positions, cos_sin, interleaved: bool, pe_out, nope_out=None, stre
         ),
         "mla_q_rope_bf16",
     )
+
+
+def qkv_a_rows(qkv, q_rank: int, q_norm_weight, kv_norm_weight, positions, cos_sin, eps: float, interleaved: bool,
+               out=None, stream=None):
+    """``qkv [T, q_rank + 576]`` (the fused q_a / kv_a output): RMSNorm of ``qkv[:, :q_rank]`` in place,
+    and the latent rows ``[T, 576]`` of ``qkv[:, q_rank:]`` (as ``latent_rows``), in one launch."""
+    import torch
+
+    assert qkv.dim() == 2 and qkv.shape[1] == q_rank + 576 and qkv.dtype == torch.bfloat16 and qkv.stride(1) == 1
+    assert qkv.is_cuda and q_rank % 8 == 0
+    T = qkv.shape[0]
+    assert q_norm_weight.shape == (q_rank,) and q_norm_weight.dtype == torch.bfloat16 and q_norm_weight.is_contiguous()
+    assert kv_norm_weight.shape == (512,) and kv_norm_weight.dtype == torch.bfloat16 and kv_norm_weight.is_contiguous()
+    assert positions.shape == (T,) and positions.dtype == torch.int32 and positions.is_contiguous()
+    assert cos_sin.dim() == 2 and cos_sin.shape[1] == 64 and cos_sin.dtype == torch.float32 and cos_sin.is_contiguous()
+    if out is None:
+        out = torch.empty((T, 576), dtype=torch.bfloat16, device=qkv.device)
+    assert out.shape == (T, 576) and out.dtype == torch.bfloat16 and out.stride(1) == 1
+    check(
+        load_library().mla_qkv_a_rows_bf16(
+            _ptr(qkv), qkv.stride(0), q_rank, _ptr(q_norm_weight), _ptr(kv_norm_weight), _ptr(positions),
+            _ptr(cos_sin), cos_sin.shape[0], T, float(eps), int(bool(interleaved)), _ptr(out), out.stride(0),
+            _stream(stream),
+        ),
+        "mla_qkv_a_rows_bf16",
+    )
+    return out

@@ -106,7 +106,9 @@ class HipLayerOps:
     ``rms_norm(x, w, eps)`` normalises the rows of a fresh projection output in place;
     ``latent_rows(kv, w, positions, cos_sin, eps, interleaved)`` -> ``[T, 576]``;
     ``q_rope(q, positions, cos_sin, interleaved, pe_out, nope_out=None)`` writes the roped rope
-    dims to ``pe_out`` (possibly in place) and, if given, the nope dims to ``nope_out``."""
+    dims to ``pe_out`` (possibly in place) and, if given, the nope dims to ``nope_out``;
+    ``qkv_a_rows`` does ``rms_norm`` of the q_a part and ``latent_rows`` of the kv part of the fused
+    q_a / kv_a output in one launch."""
 
     @staticmethod
     def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -119,6 +121,13 @@ class HipLayerOps:
     @staticmethod
     def q_rope(q, positions, cos_sin, interleaved: bool, pe_out, nope_out=None) -> None:
         lib.q_rope(q, positions, cos_sin, interleaved, pe_out, nope_out)
+
+    @staticmethod
+    def qkv_a_rows(qkv_a, q_rank: int, q_w, kv_w, positions, cos_sin, eps: float, interleaved: bool):
+        """Fused q_a / kv_a output ``[T, q_rank + 576]``: RMSNorm of the q_a part in place and the
+        latent rows ``[T, 576]``, one launch. Returns (normed q_a view, latent rows)."""
+        latent = lib.qkv_a_rows(qkv_a, q_rank, q_w, kv_w, positions, cos_sin, eps, interleaved)
+        return qkv_a[:, :q_rank], latent
 
 
 @dataclass
@@ -211,9 +220,9 @@ class MLAAttentionLayer:
         pos = batch.positions.to(torch.int32)  # no copy when the scheduler already gives int32
 
         qkv_a = x @ self.w_qkv_a.t()  # [T, q_lora + 576]
-        r = self.cfg.q_lora_rank
-        q = (ops.rms_norm(qkv_a[:, :r], self.w.q_a_norm, eps) @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
-        latent = ops.latent_rows(qkv_a[:, r:], self.w.kv_a_norm, pos, self.cos_sin, eps, inter)  # [T, 576]
+        q_a, latent = ops.qkv_a_rows(qkv_a, self.cfg.q_lora_rank, self.w.q_a_norm, self.w.kv_a_norm, pos,
+                                     self.cos_sin, eps, inter)  # normed q_a, latent rows [T, 576]
+        q = (q_a @ self.w.q_b.t()).view(T, H, a.qk_head_dim)
 
         if batch.is_decode:
             # absorbed: q_abs = [q_nope W_UK | rope(q_pe)] per head; the nope dims go head-major for the bmm

@@ -51,6 +51,11 @@ class TorchLayerOps:
                          dim=-1)
 
     @classmethod
+    def qkv_a_rows(cls, qkv_a, q_rank, q_w, kv_w, positions, cos_sin, eps, interleaved):
+        return (cls.rms_norm(qkv_a[:, :q_rank], q_w, eps),
+                cls.latent_rows(qkv_a[:, q_rank:], kv_w, positions, cos_sin, eps, interleaved))
+
+    @classmethod
     def q_rope(cls, q, positions, cos_sin, interleaved, pe_out, nope_out=None):
         pe_out.copy_(cls.rope(q[..., 128:], positions, cos_sin, interleaved))
         if nope_out is not None:

@@ -84,4 +84,6 @@ def test_layer_op_argument_errors_are_reported():
     assert rc != 0 and b"heads of 192" in so.mla_last_error()
     rc = so.mla_q_rope_bf16(p, 384, 192, 4, 2, p, p, 16, 1, p, 128, 64, p + 2, 128, 512, None)
     assert rc != 0 and b"nope_out" in so.mla_last_error()
+    rc = so.mla_qkv_a_rows_bf16(p, 2112, 1530, p, p, p, p, 16, 4, 1e-6, 1, p, 576, None)
+    assert rc != 0 and b"q_rank" in so.mla_last_error()
     assert so.mla_rmsnorm_bf16(None, 0, None, 0, 8, 1e-6, None, 0, None) == 0  # no rows: nothing to do

@@ -98,3 +98,21 @@ def test_q_rope_in_place_prefill_layout():
     assert torch.equal(q[..., :128], ref[..., :128])
     torch.testing.assert_close(q[..., 128:].float(), S.TorchLayerOps.rope(ref[..., 128:], pos, cache, True).float(),
                                **TOL)
+
+
+def test_qkv_a_rows_equals_the_separate_ops():
+    """The fused q_a / kv_a rows kernel gives the separate RMSNorm and latent-row kernels' output
+    bit for bit (same arithmetic in the same order)."""
+    gen = torch.Generator().manual_seed(13)
+    cache = rope_cos_sin_cache(64, MAX_POS, 50000.0, YARN).to(DEV)
+    for rows, q_rank in ((1, 1536), (64, 1536), (700, 384)):
+        qkv = _bf16((rows, q_rank + 576), gen)
+        q_w, kv_w = _bf16((q_rank,), gen, 0.1) + 1, _bf16((512,), gen, 0.1) + 1
+        pos = torch.randint(0, MAX_POS, (rows,), generator=gen, dtype=torch.int32).to(DEV)
+        ref_q = lib.rmsnorm(qkv[:, :q_rank], q_w, 1e-6)
+        ref_lat = lib.latent_rows(qkv[:, q_rank:], kv_w, pos, cache, 1e-6, True)
+        fused = qkv.clone()
+        lat = lib.qkv_a_rows(fused, q_rank, q_w, kv_w, pos, cache, 1e-6, True)
+        torch.cuda.synchronize()
+        assert torch.equal(fused[:, :q_rank], ref_q) and torch.equal(fused[:, q_rank:], qkv[:, q_rank:])
+        assert torch.equal(lat, ref_lat)
