@@ -37,6 +37,10 @@ from .utils import BaseCaptureData
 _CPU_I32 = {"device": "cpu", "dtype": torch.int32, "pin_memory": True}
 
 
+# the prefill kernel reads keys in 64-token tiles that must lie inside one page
+PREFILL_PAGE = 64
+
+
 @dataclass
 class MLACaptureData(BaseCaptureData):
     plan: torch.Tensor  # int32 [num_ctas * 4 + max_bs * 3]
@@ -53,6 +57,7 @@ class MLAMetadata(BaseAttnMetadata):
     is_decode: bool
     plan: torch.Tensor | None = None  # decode split-KV plan (device)
     num_slots: int = 0
+    seqlens_k: List[int] | None = None  # host copy of cache_seqlens (prefill batches)
 
     def get_last_indices(self, bs: int) -> torch.Tensor:
         return self.cu_seqlens_q[1 : 1 + bs] - 1
@@ -113,12 +118,44 @@ class MLAAttnBackend(BaseAttnBackend):
         T, H, _ = q.shape
         out = torch.empty((T, H, self.config.v_head_dim), dtype=q.dtype, device=q.device)
         lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
+        k_pages, v_pages = self.kvcache.prefill_k_cache(layer_id), self.kvcache.prefill_v_cache(layer_id)
+        page_table = metadata.page_table
+        if self.page_size < PREFILL_PAGE:
+            k_pages, v_pages, page_table = self._prefill_pages_of(k_pages, v_pages, metadata)
         lib.mla_prefill(
-            q, self.kvcache.prefill_k_cache(layer_id), self.kvcache.prefill_v_cache(layer_id), metadata.page_table,
-            metadata.cu_seqlens_q, metadata.cache_seqlens, self.scale, out, lse,
+            q, k_pages, v_pages, page_table, metadata.cu_seqlens_q, metadata.cache_seqlens, self.scale, out, lse,
         )
         self.last_lse = lse
         return out
+
+    def _prefill_pages_of(self, k_pool: torch.Tensor, v_pool: torch.Tensor, md: MLAMetadata):
+        """Pools with pages smaller than the prefill kernel's 64-token key tile (the reference's
+        default page size is 1, python/minisgl/engine/config.py:25): every request's K/V rows are
+        gathered on the device into consecutive 64-token pages of a scratch pool, with a page table
+        over it, and the prefill kernel runs on those."""
+        ps, H = self.page_size, k_pool.shape[-2]
+        lens = md.seqlens_k
+        pages = [-(-L // PREFILL_PAGE) for L in lens]
+        first = [0]
+        for n in pages:
+            first.append(first[-1] + n)
+        dev = k_pool.device
+        k_tmp = torch.empty((max(first[-1], 1), PREFILL_PAGE, H, k_pool.shape[-1]), dtype=k_pool.dtype, device=dev)
+        v_tmp = torch.empty((max(first[-1], 1), PREFILL_PAGE, H, v_pool.shape[-1]), dtype=v_pool.dtype, device=dev)
+        kf, vf = k_pool.view(-1, H * k_pool.shape[-1]), v_pool.view(-1, H * v_pool.shape[-1])
+        ktf, vtf = k_tmp.view(-1, H * k_pool.shape[-1]), v_tmp.view(-1, H * v_pool.shape[-1])
+        for b, L in enumerate(lens):
+            if L == 0:
+                continue
+            t = torch.arange(L, device=dev)
+            src = md.page_table[b, t // ps].long() * ps + t % ps  # the request's pool rows
+            dst = first[b] * PREFILL_PAGE + t
+            ktf[dst] = kf[src]
+            vtf[dst] = vf[src]
+        width = max(max(pages), 1)
+        pt = torch.tensor([[first[b] + min(j, max(n - 1, 0)) for j in range(width)] for b, n in enumerate(pages)],
+                          dtype=torch.int32).to(dev, non_blocking=True)
+        return k_tmp, v_tmp, pt
 
     # ------------------------------------------------------------------ metadata
     def prepare_metadata(self, batch: Batch) -> None:
@@ -160,6 +197,7 @@ class MLAAttnBackend(BaseAttnBackend):
             is_decode=is_decode,
             plan=plan_dev,
             num_slots=slots,
+            seqlens_k=None if is_decode else seqlens_k,
         )
 
     # ------------------------------------------------------------------ graph capture

@@ -123,11 +123,15 @@ def test_backend_decode_graph_replay():
             r.complete_one()
 
 
-def test_backend_prefill_with_prefix():
+@pytest.mark.parametrize("page_size", [64, 32, 16, 1])
+def test_backend_prefill_with_prefix(page_size):
     """A prefill batch through the backend: the new per-head K/V rows are stored
-    at out_loc, then every request attends its cached prefix and itself causally."""
+    at out_loc, then every request attends its cached prefix and itself causally.
+    Pages smaller than 64 tokens (the reference's default page size is 1) go through
+    the backend's gather into 64-token scratch pages."""
+    print(f"[backend prefill] page_size={page_size}", flush=True)
     reset_global_ctx()
-    page_size, H = 64, 16
+    H = 16
     ctx = Context(page_size=page_size)
     set_global_ctx(ctx)
     gen = torch.Generator().manual_seed(5)

@@ -79,6 +79,13 @@ def test_mla_layer_kimi_k2_shape():
     _run_case(H=64, hidden=7168, q_lora=1536, steps=steps, seed=1)
 
 
+def test_mla_layer_page_size_one():
+    """The reference's default page size (1): decode on token pages, prefill through 64-token
+    scratch pages gathered by the backend."""
+    steps = [("prefill", {0: 90, 1: 40}), ("decode", {0: 1, 1: 1}), ("prefill", {1: 70}), ("decode", {0: 1, 1: 1})]
+    _run_case(H=16, hidden=1024, q_lora=384, steps=steps, page_size=1, seed=7)
+
+
 def test_mla_layer_kimi_k2_tp8_shard():
     """Kimi-K2's attention over 8 GPUs: 8 heads per GPU, hidden 7168."""
     steps = [("prefill", {0: 90, 1: 40}), ("decode", {0: 1, 1: 1}), ("decode", {0: 1, 1: 1})]
