@@ -58,6 +58,7 @@ class MLAMetadata(BaseAttnMetadata):
     plan: torch.Tensor | None = None  # decode split-KV plan (device)
     num_slots: int = 0
     seqlens_k: List[int] | None = None  # host copy of cache_seqlens (prefill batches)
+    num_ctas: int = 0  # CTAs the decode plan was made for (0: the backend's default)
 
     def get_last_indices(self, bs: int) -> torch.Tensor:
         return self.cu_seqlens_q[1 : 1 + bs] - 1
@@ -73,12 +74,14 @@ class MLAAttnBackend(BaseAttnBackend):
         self.device = self.kvcache.device
         self.scale = config.softmax_scale
         self.num_heads = config.num_heads
-        dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
-        # one persistent decode CTA per compute unit
-        self.num_ctas = num_ctas or lib.device_cu_count(dev_index)
+        if num_ctas is None:  # one persistent decode CTA per compute unit
+            dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+            num_ctas = lib.device_cu_count(dev_index)
+        self.num_ctas = num_ctas
         self.capture: MLACaptureData | None = None
         self.capture_bs: List[int] = []
         self.max_graph_bs = 0
+        self.capture_ctas = self.num_ctas
         self.ws_o: torch.Tensor | None = None
         self.ws_lse: torch.Tensor | None = None
         self.last_lse: torch.Tensor | None = None  # natural-log LSE of the last forward
@@ -105,7 +108,7 @@ class MLAAttnBackend(BaseAttnBackend):
         lse = torch.empty((B, H), dtype=torch.float32, device=q.device)
         lib.mla_decode(
             q, self.kvcache.latent_cache(layer_id), metadata.page_table, metadata.cache_seqlens, metadata.plan,
-            self.num_ctas, self.ws_o, self.ws_lse, self.scale, out, lse,
+            metadata.num_ctas or self.num_ctas, self.ws_o, self.ws_lse, self.scale, out, lse,
         )
         self.last_lse = lse
         return out
@@ -157,6 +160,19 @@ class MLAAttnBackend(BaseAttnBackend):
                           dtype=torch.int32).to(dev, non_blocking=True)
         return k_tmp, v_tmp, pt
 
+    def _plan(self, seqlens_k: List[int], ctas: int):
+        """Split plan on ``ctas`` CTAs, doubling the count while the batch does not fit: with pages
+        under 32 tokens a piece holds at most MAX_PIECE_PAGES tokens' page ids, so a long batch can
+        need more pieces than compute units (the extra CTAs run as further rounds)."""
+        while True:
+            try:
+                plan_np, slots = lib.decode_plan(seqlens_k, self.page_size, ctas)
+                return plan_np, slots, ctas
+            except lib.MLAKernelError as e:
+                if "cannot hold" not in str(e) or ctas >= 64 * self.num_ctas:
+                    raise
+                ctas *= 2
+
     # ------------------------------------------------------------------ metadata
     def prepare_metadata(self, batch: Batch) -> None:
         reqs = batch.padded_reqs
@@ -181,10 +197,11 @@ class MLAAttnBackend(BaseAttnBackend):
         page_table = lib.page_table_from_tokens(get_global_ctx().page_table, table_idx, max_seqlen_k, self.page_size)
 
         is_decode = batch.is_decode
-        plan_dev, slots = None, 0
+        plan_dev, slots, ctas = None, 0, 0
         if is_decode:
             assert max_seqlen_q == 1, "decode batches extend every request by one token"
-            plan_np, slots = lib.decode_plan(seqlens_k, self.page_size, self.num_ctas)
+            graphed = self.capture is not None and padded_size <= self.max_graph_bs
+            plan_np, slots, ctas = self._plan(seqlens_k, self.capture_ctas if graphed else self.num_ctas)
             self._ensure_workspace(max(slots, 1))
             plan_dev = torch.from_numpy(plan_np).pin_memory().to(device, non_blocking=True)
         batch.attn_metadata = MLAMetadata(
@@ -198,6 +215,7 @@ class MLAAttnBackend(BaseAttnBackend):
             plan=plan_dev,
             num_slots=slots,
             seqlens_k=None if is_decode else seqlens_k,
+            num_ctas=ctas if is_decode else 0,
         )
 
     # ------------------------------------------------------------------ graph capture
@@ -205,10 +223,12 @@ class MLAAttnBackend(BaseAttnBackend):
         assert self.capture is None, "Capture already initialized."
         max_bs = max(bs_list)
         cols = -(-max_seq_len // self.page_size)
-        plan = torch.zeros((self.num_ctas * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS,), dtype=torch.int32,
+        # the captured launch has a fixed grid: size it for the longest batch the graphs can see
+        _, _, self.capture_ctas = self._plan([max_seq_len] * max_bs, self.num_ctas)
+        plan = torch.zeros((self.capture_ctas * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS,), dtype=torch.int32,
                            device=self.device)
         # a plan never needs more partial slots than CTAs plus requests
-        self._ensure_workspace(self.num_ctas + max_bs)
+        self._ensure_workspace(self.capture_ctas + max_bs)
         self.capture = MLACaptureData.create(max_bs, cols, self.device, plan=plan)
         self.max_graph_bs = max_bs
         self.capture_bs = sorted(bs_list)
@@ -216,7 +236,7 @@ class MLAAttnBackend(BaseAttnBackend):
     def prepare_for_capture(self, batch: Batch) -> None:
         assert (bs := batch.size) in self.capture_bs and self.capture is not None
         cap = self.capture
-        plan_np, _ = lib.decode_plan([r.device_len for r in batch.reqs], self.page_size, self.num_ctas)
+        plan_np, _ = lib.decode_plan([r.device_len for r in batch.reqs], self.page_size, self.capture_ctas)
         n = plan_np.shape[0]
         cap.plan[:n].copy_(torch.from_numpy(plan_np))
         batch.attn_metadata = MLAMetadata(
@@ -229,6 +249,7 @@ class MLAAttnBackend(BaseAttnBackend):
             is_decode=True,
             plan=cap.plan,
             num_slots=self.ws_o.shape[0],
+            num_ctas=self.capture_ctas,
         )
 
     def prepare_for_replay(self, batch: Batch) -> None:
@@ -240,6 +261,7 @@ class MLAAttnBackend(BaseAttnBackend):
         cap.cu_seqlens_k[: bs + 1].copy_(metadata.cu_seqlens_k)
         cap.seq_lens[:bs].copy_(metadata.cache_seqlens)
         cap.page_table[:bs, :table_len].copy_(metadata.page_table)
+        assert metadata.num_ctas == self.capture_ctas, "replayed batches are planned for the captured grid"
         cap.plan[: metadata.plan.numel()].copy_(metadata.plan)
 
 

@@ -182,3 +182,41 @@ def test_backend_prefill_with_prefix(page_size):
     torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
     md = batch.attn_metadata
     assert torch.equal(md.get_last_indices(len(reqs)).cpu(), cu[1:] - 1)
+
+
+def test_backend_decode_page_size_one_kimi_batch():
+    """The reference's default page size (1) with the Kimi-K2 batch (B=64, L~U[1024,8192]): a piece
+    holds at most 1024 page ids, so the backend plans 512 CTAs (two rounds over the compute
+    units) rather than failing; output against the oracle."""
+    from minisgl_amd.benchmark.inputs import make_decode_case
+
+    reset_global_ctx()
+    case = make_decode_case(64, 64, 1, len_range=(1024, 8192), seed=0)
+    ctx = Context(page_size=1)
+    set_global_ctx(ctx)
+    cfg = MLAConfig(num_heads=64, num_layers=1)
+    num_pages = case.kv_pool.shape[0]
+    pool = create_kvcache_pool(cfg, num_pages, 1, torch.bfloat16, DEV)
+    pool.latent_cache(0).copy_(case.kv_pool.to(DEV))
+    ctx.kv_cache = pool
+    width = -(-case.page_table.shape[1] // 32) * 32
+    tt = torch.zeros((65, width), dtype=torch.int32)
+    tt[:64, : case.page_table.shape[1]] = case.page_table  # page size 1: token location == page id
+    ctx.page_table = tt.to(DEV)
+    backend = create_attention_backend("mla", cfg)
+    ctx.attn_backend = backend
+    reqs = [Req(table_idx=i, cached_len=L - 1, device_len=L) for i, L in enumerate(case.lens)]
+    batch = Batch(reqs=reqs, phase="decode")
+    batch.padded_reqs = reqs
+    batch.out_loc = torch.tensor([int(tt[i, L - 1]) for i, L in enumerate(case.lens)], dtype=torch.int32, device=DEV)
+    backend.prepare_metadata(batch)
+    assert batch.attn_metadata.num_ctas > backend.num_ctas
+    print(f"[backend ps=1] ctas={batch.attn_metadata.num_ctas}", flush=True)
+    k_new = pool.latent_cache(0).view(-1, 576)[batch.out_loc.long()].clone()  # re-store the same rows
+    with ctx.forward_batch(batch):
+        o = backend.forward(case.q.to(DEV), k_new, None, 0, batch)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = R.mla_decode(case.q, case.kv_pool, case.page_table, case.lens)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
+    reset_global_ctx()

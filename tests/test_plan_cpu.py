@@ -77,3 +77,29 @@ def test_plan_long_context_and_piece_cap():
 def test_plan_rejects_impossible():
     with pytest.raises(lib.MLAKernelError):
         lib.decode_plan([100000], 1, 2)
+
+
+def test_backend_plans_more_ctas_for_small_pages():
+    """With pages under 32 tokens a piece holds at most MAX_PIECE_PAGES tokens, so the Kimi-K2 batch
+    (336807 tokens) needs more pieces than 256 CTAs: the backend doubles the CTA count (the extra
+    CTAs run as further rounds) instead of failing; page size 64 keeps one CTA per compute unit."""
+    import torch
+
+    from minisgl_amd.attention.mla import MLAAttnBackend
+    from minisgl_amd.benchmark.layer import decode_lens
+    from minisgl_amd.config import MLAConfig
+    from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
+    from minisgl_amd.kvcache import create_kvcache_pool
+
+    lens = decode_lens()
+    with pytest.raises(lib.MLAKernelError, match="cannot hold"):
+        lib.decode_plan(lens, 1, 256)
+    for ps, want in ((1, 512), (64, 256)):
+        reset_global_ctx()
+        ctx = Context(page_size=ps)
+        set_global_ctx(ctx)
+        ctx.kv_cache = create_kvcache_pool(MLAConfig(num_layers=1), 4, ps, torch.bfloat16, "cpu")
+        be = MLAAttnBackend(MLAConfig(num_layers=1), num_ctas=256)
+        plan, slots, ctas = be._plan(lens, 256)
+        assert ctas == want and plan.shape[0] == ctas * lib.PLAN_CTA_INTS + len(lens) * lib.PLAN_REQ_INTS
+        reset_global_ctx()
