@@ -78,11 +78,16 @@ def test_backend_decode_eager():
     assert torch.equal(md.get_last_indices(len(reqs)).cpu(), torch.arange(len(reqs), dtype=torch.int32))
 
 
-def test_backend_decode_graph_replay():
-    ctx, cfg, pool, backend, reqs, tt, max_req = _setup(seed=2)
+@pytest.mark.parametrize("page_size,graph_max_len", [(64, 4096), (1, 65536)])
+def test_backend_decode_graph_replay(page_size, graph_max_len):
+    """Capture and replay; at page size 1 the graphs' longest batch (8 x 65536 tokens) needs more
+    pieces than compute units, so the captured grid is 512 CTAs."""
+    print(f"[graph replay] page_size={page_size}", flush=True)
+    ctx, cfg, pool, backend, reqs, tt, max_req = _setup(page_size=page_size, seed=2)
     bs = 8
     dummy = Req(table_idx=max_req, cached_len=0, device_len=1)
-    backend.init_capture_graph(max_seq_len=4096, bs_list=[bs])
+    backend.init_capture_graph(max_seq_len=graph_max_len, bs_list=[bs])
+    assert backend.capture_ctas == (backend.num_ctas if page_size >= 32 else 2 * backend.num_ctas)
     q_static = torch.zeros((bs, 64, 576), dtype=torch.bfloat16, device=DEV)
     k_static = torch.zeros((bs, 576), dtype=torch.bfloat16, device=DEV)
     loc_static = torch.full((bs,), int(tt[max_req, 0]), dtype=torch.int32, device=DEV)
