@@ -69,6 +69,17 @@ int mla_store_rows(void *cache, int64_t cache_rows, int64_t cache_row_stride_byt
                    int32_t index_bits, int64_t num_rows, int64_t row_bytes, void *stream);
 
 /*
+ * out[i, :] = cache[indices[i], :] for i < num_rows (int64 indices; rows of row_bytes, a multiple of
+ * 16; strides in bytes). The inverse of mla_store_rows; rows whose index lies outside
+ * [0, cache_rows) are left untouched. Used to gather a request's per-head K/V rows from pools
+ * with pages under 64 tokens into the 64-token pages the prefill kernel reads (the gather the
+ * FA backend's paged reads do, python/minisgl/attention/fa.py:157-182).
+ */
+int mla_gather_rows(void *out, int64_t out_row_stride_bytes, const void *cache, int64_t cache_rows,
+                    int64_t cache_row_stride_bytes, const int64_t *indices, int64_t num_rows, int64_t row_bytes,
+                    void *stream);
+
+/*
  * Token table -> page table, bit-exact:
  *   out[b, j] = token_table[table_idx[b], j * page_size] / page_size
  * for j < ceil(max_seqlen_k / page_size). Replaces the slicing in

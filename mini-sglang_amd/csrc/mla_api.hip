@@ -87,6 +87,25 @@ int mla_store_rows(void* cache, int64_t cache_rows, int64_t cache_row_stride_byt
                     "mla_store_rows launch");
 }
 
+int mla_gather_rows(void* out, int64_t out_row_stride_bytes, const void* cache, int64_t cache_rows,
+                    int64_t cache_row_stride_bytes, const int64_t* indices, int64_t num_rows, int64_t row_bytes,
+                    void* stream) {
+  const char* who = "mla_gather_rows";
+  if (num_rows < 0) return fail(MLA_ERR_INVALID_ARG, "%s: num_rows < 0", who);
+  if (num_rows == 0) return ok();
+  if (out == nullptr || cache == nullptr || indices == nullptr) return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (row_bytes <= 0 || row_bytes % 16 != 0)
+    return fail(MLA_ERR_UNSUPPORTED, "%s: row_bytes %lld is not a positive multiple of 16", who, (long long)row_bytes);
+  if (out_row_stride_bytes < row_bytes || out_row_stride_bytes % 16 != 0 || cache_row_stride_bytes < row_bytes ||
+      cache_row_stride_bytes % 16 != 0)
+    return fail(MLA_ERR_INVALID_ARG, "%s: strides must be multiples of 16 and >= row_bytes", who);
+  if (!aligned(out, 16) || !aligned(cache, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: 16-byte alignment", who);
+  if (cache_rows <= 0) return fail(MLA_ERR_INVALID_ARG, "%s: cache_rows must be positive", who);
+  return hip_status(mla::launch_gather_rows(out, out_row_stride_bytes, cache, cache_rows, cache_row_stride_bytes, indices,
+                                            num_rows, row_bytes, (hipStream_t)stream),
+                    "mla_gather_rows launch");
+}
+
 int mla_page_table_from_tokens(const int32_t* token_table, int32_t token_table_rows, int32_t token_table_cols,
                                int64_t token_table_stride, const int32_t* table_idx, int32_t batch,
                                int32_t max_seqlen_k, int32_t page_size, int32_t* out, int64_t out_stride,

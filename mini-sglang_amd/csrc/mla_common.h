@@ -103,6 +103,9 @@ hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
 hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
                              const void* indices, int index_bits, int64_t rows, int64_t row_bytes,
                              hipStream_t stream);
+hipError_t launch_gather_rows(void* out, int64_t out_stride, const void* cache, int64_t cache_rows,
+                              int64_t cache_stride, const int64_t* indices, int64_t rows, int64_t row_bytes,
+                              hipStream_t stream);
 hipError_t launch_page_table(const int32_t* tt, int32_t tt_rows, int64_t tt_stride, const int32_t* table_idx,
                              int32_t batch, int32_t cols, int32_t page_size, int32_t* out,
                              int64_t out_stride, hipStream_t stream);

@@ -26,6 +26,24 @@ __global__ __launch_bounds__(256) void store_rows_kernel(char* __restrict__ cach
   }
 }
 
+// out[i] = cache[indices[i]] (the inverse of store_rows): the grid covers (row, 16-byte chunk)
+// pairs; rows whose index lies outside the cache are left untouched.
+__global__ __launch_bounds__(256) void gather_rows_kernel(char* __restrict__ out, int64_t out_stride,
+                                                          const char* __restrict__ cache, int64_t cache_rows,
+                                                          int64_t cache_stride, const int64_t* __restrict__ indices,
+                                                          int64_t rows, int64_t chunks_per_row) {
+  const int64_t total = rows * chunks_per_row;
+  for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
+       id += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = id / chunks_per_row;
+    const int64_t ch = id - r * chunks_per_row;
+    const int64_t src_row = indices[r];
+    if (src_row < 0 || src_row >= cache_rows) continue;
+    *reinterpret_cast<u32x4*>(out + r * out_stride + ch * 16) =
+        *reinterpret_cast<const u32x4*>(cache + src_row * cache_stride + ch * 16);
+  }
+}
+
 // out[b, j] = floor(tt[table_idx[b], j * ps] / ps)
 __global__ __launch_bounds__(256) void page_table_kernel(const int32_t* __restrict__ tt, int32_t tt_rows,
                                                          int64_t tt_stride,
@@ -58,6 +76,18 @@ hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stri
   else
     hipLaunchKernelGGL(store_rows_kernel<int64_t>, dim3(grid), dim3(256), 0, stream, (char*)cache, cache_rows, cache_stride,
                        (const char*)x, x_stride, (const int64_t*)indices, rows, cpr);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(void* out, int64_t out_stride, const void* cache, int64_t cache_rows,
+                              int64_t cache_stride, const int64_t* indices, int64_t rows, int64_t row_bytes,
+                              hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  const int64_t cpr = row_bytes / 16;
+  const int64_t want = (rows * cpr + 255) / 256;
+  const int grid = (int)(want < 65536 ? want : 65536);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(grid), dim3(256), 0, stream, (char*)out, out_stride, (const char*)cache,
+                     cache_rows, cache_stride, indices, rows, cpr);
   return hipGetLastError();
 }
 

@@ -152,9 +152,9 @@ class MLAAttnBackend(BaseAttnBackend):
                 continue
             t = torch.arange(L, device=dev)
             src = md.page_table[b, t // ps].long() * ps + t % ps  # the request's pool rows
-            dst = first[b] * PREFILL_PAGE + t
-            ktf[dst] = kf[src]
-            vtf[dst] = vf[src]
+            dst0 = first[b] * PREFILL_PAGE
+            lib.gather_rows(ktf[dst0 : dst0 + L], kf, src)
+            lib.gather_rows(vtf[dst0 : dst0 + L], vf, src)
         width = max(max(pages), 1)
         pt = torch.tensor([[first[b] + min(j, max(n - 1, 0)) for j in range(width)] for b, n in enumerate(pages)],
                           dtype=torch.int32).to(dev, non_blocking=True)

@@ -28,6 +28,7 @@ SIGNATURES = {
     "mla_abi_version": (ctypes.c_int, []),
     "mla_device_cu_count": (ctypes.c_int, [ctypes.c_int, _c_i32p]),
     "mla_store_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp]),
+    "mla_gather_rows": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
     "mla_page_table_from_tokens": (
         ctypes.c_int,
         [_vp, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _vp],
@@ -353,3 +354,23 @@ def qkv_a_rows(qkv, q_rank: int, q_norm_weight, kv_norm_weight, positions, cos_s
         "mla_qkv_a_rows_bf16",
     )
     return out
+
+
+def gather_rows(out, cache, indices, stream=None) -> None:
+    """``out[i] = cache[indices[i]]`` over the leading dims (int64 indices; the inverse of store_rows)."""
+    import torch
+
+    assert out.is_cuda and cache.is_cuda and indices.is_cuda and out.dtype == cache.dtype
+    assert indices.dim() == 1 and indices.dtype == torch.int64 and indices.is_contiguous()
+    n = indices.shape[0]
+    o2, c2 = out.view(out.shape[0], -1), cache.view(cache.shape[0], -1)
+    row_bytes = c2.shape[1] * c2.element_size()
+    assert o2.shape[1] * o2.element_size() == row_bytes and o2.shape[0] >= n
+    assert o2.stride(-1) == 1 and c2.stride(-1) == 1
+    check(
+        load_library().mla_gather_rows(
+            _ptr(o2), o2.stride(0) * o2.element_size(), _ptr(c2), c2.shape[0], c2.stride(0) * c2.element_size(),
+            _ptr(indices), n, row_bytes, _stream(stream),
+        ),
+        "mla_gather_rows",
+    )

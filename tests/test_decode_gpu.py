@@ -258,3 +258,20 @@ def test_decode_long_context_split_kv():
     o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
     torch.testing.assert_close(out, o_ref, **O_TOL)
     torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
+
+
+@pytest.mark.parametrize("row_elems", [576, 16 * 192])
+def test_gather_rows_bit_exact(row_elems):
+    """mla_gather_rows: out[i] = cache[idx[i]] bit for bit (the inverse of store_rows), repeated and
+    out-of-range indices included (an out-of-range row is left untouched)."""
+    g = torch.Generator().manual_seed(row_elems)
+    cache = torch.randn((300, row_elems), generator=g).to(torch.bfloat16).to(DEV)
+    idx = torch.randint(0, 300, (257,), generator=g)
+    idx[5] = idx[6]
+    idx[9] = 300  # out of range
+    out = torch.full((257, row_elems), 3.0, dtype=torch.bfloat16, device=DEV)
+    lib.gather_rows(out, cache, idx.to(DEV))
+    torch.cuda.synchronize()
+    ok = idx < 300
+    assert torch.equal(out[ok.to(DEV)].view(torch.int16), cache[idx[ok].to(DEV)].view(torch.int16))
+    assert torch.all(out[9] == 3.0)
