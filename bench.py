@@ -14,7 +14,9 @@ Prints one JSON line. ``value`` is the whole-step algorithmic HBM bandwidth
 (TB/s); µs/layer and tokens/s are extra fields. ``roofline`` times the
 dominant kernel (the split kernel) alone, 16 back-to-back launches per HIP
 graph, with HIP events on its launch stream.
-``cpu_baseline`` times the CPU oracle on a bounded sample of the same batch.
+``cpu_baseline`` times the CPU oracle on the CPU decode workload (B=4, 16
+heads, page 1, lengths U[64, 512]); ``measured_peaks`` holds a read-only HBM
+stream and a bf16 MFMA loop measured on the same GPU.
 Extra fields: the prefill attention batch, a long-context batch, a mixed
 ragged batch, and ``layer``: whole Kimi-K2 MLA layer steps (projections,
 RoPE, absorption, attention kernels, o_proj) for the same decode and prefill
@@ -56,43 +58,75 @@ def _decode_workload(device, seed):
     return make_decode_case(64, 64, 64, len_range=(1024, 8192), device=device, seed=seed)
 
 
-def _cpu_baseline(case_gpu, budget_s: float = 12.0):
-    """Oracle (fp32 torch on the host cores) on the first n requests of the batch."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """Threads for the CPU oracle: the host cores this process may use (its affinity mask, or the
+    OMP_NUM_THREADS share a shared GPU host gives one GPU's job), not every core of the host."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(omp))) if omp and omp.isdigit() else max(1, n)
+
+
+def _cpu_baseline(case_gpu, runs: int = 10):
+    """The CPU oracle (oracle/ref_mla.py, fp32 torch) on the CPU workload of the decode path: B=4,
+    16 heads, page size 1, lengths U[64, 512] (warm-up, then the median of ``runs`` runs), plus one
+    sample of the headline batch's first requests for scale."""
+    import statistics
+
     import torch
 
+    from minisgl_amd.benchmark.inputs import make_decode_case
     from oracle import ref_mla as R
 
-    cores = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(cores)
-    q = case_gpu.q.cpu()
-    kv = case_gpu.kv_pool.cpu()
-    pt = case_gpu.page_table.cpu()
-    lens = case_gpu.lens
-    R.mla_decode(q[:1], kv, pt[:1], lens[:1])  # warm-up
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    c1 = make_decode_case(4, 16, 1, len_range=(64, 512), seed=0)
+    R.mla_decode(c1.q, c1.kv_pool, c1.page_table, c1.lens)  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        R.mla_decode(c1.q, c1.kv_pool, c1.page_table, c1.lens)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    alg1 = c1.algorithmic_bytes()
+
+    # the headline batch's first requests, one run (about a second of CPU work)
+    q, kv, pt, lens = case_gpu.q.cpu(), case_gpu.kv_pool.cpu(), case_gpu.page_table.cpu(), case_gpu.lens
+    n = 8
     t0 = time.perf_counter()
-    R.mla_decode(q[:1], kv, pt[:1], lens[:1])
-    per_req = max(time.perf_counter() - t0, 1e-4)
-    n = int(max(1, min(len(lens), budget_s / per_req)))
-    reps, elapsed = 0, 0.0
-    t0 = time.perf_counter()
-    while True:
-        R.mla_decode(q[:n], kv, pt[:n], lens[:n])
-        reps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed > budget_s or reps >= 3:
-            break
-    sec = elapsed / reps
+    R.mla_decode(q[:n], kv, pt[:n], lens[:n])
+    sec2 = time.perf_counter() - t0
     H = q.shape[1]
     pages = sum(-(-L // 64) for L in lens[:n])
-    sample_bytes = sum(lens[:n]) * 1152 + n * H * (576 + 512) * 2 + n * H * 4 + pages * 4 + 4 * n
+    bytes2 = sum(lens[:n]) * 1152 + n * H * (576 + 512) * 2 + n * H * 4 + pages * 4 + 4 * n
     return {
-        "value": sample_bytes / sec / 1e12,
+        "value": alg1 / sec / 1e12,
         "unit": "TB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": f"CPU oracle (oracle/ref_mla.py, fp32 torch) on requests 0..{n - 1} of the same batch "
-        f"({sum(lens[:n])} KV tokens), {reps} run(s), {sec * 1e3:.1f} ms each",
-        "us_per_layer_sample": sec * 1e6,
+        "sample": f"CPU oracle (oracle/ref_mla.py, fp32 torch, {threads} threads) on the CPU decode workload: "
+        f"B=4, 16 heads, page 1, lengths {c1.lens} ({sum(c1.lens)} KV tokens); median of {runs} runs",
+        "us_per_layer": round(sec * 1e6, 1),
+        "tokens_per_s": round(4 / sec, 1),
+        "cpu_model": _cpu_model(),
+        "host_cpu_count": os.cpu_count(),
+        "headline_sample": {
+            "requests": n,
+            "kv_tokens": sum(lens[:n]),
+            "ms": round(sec2 * 1e3, 1),
+            "tb_per_s": round(bytes2 / sec2 / 1e12, 6),
+            "gpu_over_cpu_note": "same batch shape as the GPU line (64 heads, page 64), first 8 requests",
+        },
     }
 
 
@@ -169,13 +203,19 @@ def bench_decode(args):
         g_check.replay()
         stream.synchronize()
         assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16)), "graph replay differs from eager"
-        g_steps = capture(layer, args.steps)
+        # steady state: a graph of 10 steps (inputs alternating) replayed back to back between HIP events
+        per_replay = 10
+        g_steps = capture(layer, per_replay)
         g_steps.replay()
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        g_steps.replay()
+        replays = max(3, args.steps // per_replay)
+        ga, gb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ga.record(stream)
+        for _ in range(replays):
+            g_steps.replay()
+        gb.record(stream)
         torch.cuda.synchronize()
-        graph_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+        graph_ms = ga.elapsed_time(gb) / (replays * per_replay)
 
         # ---- each kernel alone: back-to-back launches in one graph, HIP events on its stream
         per_graph = 16
@@ -231,6 +271,7 @@ def bench_decode(args):
         "us_per_layer": round(step_ms * 1e3, 2),
         "us_per_layer_device": round(dev_step_ms * 1e3, 2),
         "us_per_layer_graph": round(graph_ms * 1e3, 2),
+        "graph_timing": "steady state: 10-step graphs replayed back to back between HIP events",
         "tokens_per_s": round(B / (step_ms * 1e-3), 1),
         "split_kernel_us": round(split_ms * 1e3, 2),
         "merge_kernel_us": round(merge_ms * 1e3, 2),
@@ -419,6 +460,23 @@ def bench_mixed(args):
         s1.wait_event(ev2)
 
     par_ms = _time_device(both, s1, steps, warm)
+    # roofline of the step: decode bytes (every page a decode row reads, counted once per row =
+    # logical, or once per distinct page = unique: the shared prefix pages are read by several rows)
+    # at 8 TB/s plus the prefill's unmasked FLOPs at 2.5 PFLOP/s
+    d = m.decode
+    H = d.q.shape[1]
+    small = d.q.shape[0] * H * (576 + 512) * 2 + d.q.shape[0] * H * 4 + 4 * d.q.shape[0]
+    logical = sum(d.lens) * 1152 + sum(-(-L // 64) for L in d.lens) * 4 + small
+    seen, unique_tokens = set(), 0
+    for b, L in enumerate(d.lens):
+        row = d.page_table[b].tolist()
+        for j in range(-(-L // 64)):
+            if row[j] not in seen:
+                seen.add(row[j])
+                unique_tokens += min(64, L - 64 * j)
+    unique = unique_tokens * 1152 + sum(-(-L // 64) for L in d.lens) * 4 + small
+    flops = m.prefill.flops()
+    t_roof_us = (unique / (HBM_PEAK_GBPS * 1e9) + flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)) * 1e6
     res = {
         "workload": "mixed ragged batch, one layer: 32 decode (ctx U[512,16384]) + 4 prefill chunks of 1024 on "
         "2048-token shared prefixes (8 groups), H=64, page 64",
@@ -427,6 +485,13 @@ def bench_mixed(args):
         "one_stream_us_per_layer": round(seq_ms * 1e3, 1),
         "two_streams_us_per_layer": round(par_ms * 1e3, 1),
         "tokens_per_layer": len(m.decode.lens) + sum(m.prefill.extends),
+        "decode_bytes_logical": logical,
+        "decode_bytes_unique": unique,
+        "prefill_flops": flops,
+        "t_roof_us": round(t_roof_us, 1),
+        "roofline_frac_one_stream": round(t_roof_us / (seq_ms * 1e3), 4),
+        "roofline_frac_two_streams": round(t_roof_us / (par_ms * 1e3), 4),
+        "t_roof_formula": "unique decode bytes / 8 TB/s + prefill unmasked FLOPs / 2.5 PFLOP/s",
     }
     del m, dec, pre
     torch.cuda.empty_cache()
@@ -492,25 +557,44 @@ def bench_layer(args):
     return res
 
 
+def bench_peaks(args):
+    """Measured peaks alone: the read-only HBM stream and the bf16 MFMA loop."""
+    from minisgl_amd.benchmark import peaks
+    from minisgl_amd.kernel import lib
+
+    cus = lib.device_cu_count(0)
+    return {"hbm_read": peaks.hbm_read(cus), "mfma_bf16": peaks.mfma_bf16(cus)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed", "layer"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed", "layer", "peaks"])
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill summary of the decode line")
     ap.add_argument("--no-extra", action="store_true", help="skip the long-context and mixed-batch summaries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured HBM-read and MFMA peaks")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part "
               "of this build", file=sys.stderr)
         sys.exit(2)
-    one = {"prefill": bench_prefill, "long": bench_long_context, "mixed": bench_mixed, "layer": bench_layer}
+    one = {"prefill": bench_prefill, "long": bench_long_context, "mixed": bench_mixed, "layer": bench_layer,
+           "peaks": bench_peaks}
     if args.workload in one:
         print(json.dumps(one[args.workload](args)))
         return
     res = bench_decode(args)
+    if not args.no_peaks:
+        from minisgl_amd.benchmark import peaks
+        from minisgl_amd.kernel import lib
+
+        cus = lib.device_cu_count(0)
+        res["measured_peaks"] = {"hbm_read": peaks.hbm_read(cus), "mfma_bf16": peaks.mfma_bf16(cus)}
+        res["roofline"]["frac_of_measured_read_peak"] = round(
+            res["roofline"]["achieved"] / 1e3 / res["measured_peaks"]["hbm_read"]["tb_per_s"], 4)
     if not args.no_prefill:
         res["prefill"] = bench_prefill(args)
     if not args.no_extra:

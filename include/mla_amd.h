@@ -103,7 +103,14 @@ int mla_page_table_from_tokens(const int32_t *token_table, int32_t token_table_r
  *   cta_ranges[num_ctas*4] : {req_begin, blk_begin, req_end, blk_end} (end exclusive)
  *   req_info[batch*3]      : {first_cta, num_pieces, slot_base}
  *   *num_slots             : partial-result slots the plan needs in the workspace
- * Pieces are at most max_piece_pages pages long.
+ * A piece touches at most max_piece_pages pages (<= 0: no limit; the kernels take pieces of
+ * any length). A CTA's range holds at most MLA_PLAN_MAX_CTA_BLOCKS blocks and
+ * MLA_PLAN_MAX_CTA_REQUESTS requests; a batch that num_ctas CTAs cannot hold within these
+ * limits fails with MLA_ERR_UNSUPPORTED ("cannot hold"). A split request's pieces sit in
+ * consecutive CTAs, and no CTA holds more than two pieces of split requests, so
+ * *num_slots <= 2 * num_ctas. CTAs past the last one used get the empty range
+ * {batch, 0, batch, 0}; a plan for n CTAs runs unchanged on a grid of m > n CTAs once its
+ * cta_ranges are extended with such empty ranges (req_info then starts at m*4).
  */
 int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
                     int32_t num_ctas, int32_t max_piece_pages, int32_t *cta_ranges,

@@ -18,6 +18,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "minisgl_amd", "kernel", "libmla_amd.so")
+# measured-peak kernels of the benchmark: a separate library, not part of libmla_amd's ABI
+PEAKS_SRC = os.path.join(CSRC, "peaks", "mla_peaks.hip")
+PEAKS_OUT = os.path.join(HERE, "minisgl_amd", "benchmark", "libmla_peaks.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # packed-fp32 VALU forms are disabled for all device code built here.
@@ -49,20 +52,25 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    jobs = jobs or min(8, len(sources))
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = OUT + ".tmp"
+def _link(objs, out: str) -> None:
+    tmp = out + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    jobs = jobs or min(8, len(sources) + 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, sources + [PEAKS_SRC]))
+    _link(objs[:-1], OUT)
+    _link(objs[-1:], PEAKS_OUT)
     if verbose:
-        print(f"built {OUT} from {len(sources)} sources")
+        print(f"built {OUT} from {len(sources)} sources, and {PEAKS_OUT}")
     return OUT
 
 

@@ -213,14 +213,14 @@ int mla_decode_plan(const int32_t* seq_lens, int32_t batch, int32_t page_size, i
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: batch < 0");
   if (num_ctas < 1) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: num_ctas must be >= 1");
   if (!is_pow2(page_size)) return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: page_size %d is not a power of two", page_size);
-  if (max_piece_pages < 1 || max_piece_pages > mla::kMaxPieceIds)
-    return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: max_piece_pages must be in [1, %d]", mla::kMaxPieceIds);
   if (cta_ranges == nullptr || num_slots == nullptr || (batch > 0 && (seq_lens == nullptr || req_info == nullptr)))
     return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: null pointer");
   const int B = mla::kPlanBlock;
-  // Longest piece in blocks such that the pages it touches fit the LDS id buffer.
-  const int64_t max_blk = page_size <= B ? (int64_t)max_piece_pages * page_size / B
-                                         : (int64_t)(max_piece_pages - 1) * page_size / B;
+  // Longest piece in blocks such that it touches at most max_piece_pages pages (no limit if <= 0;
+  // the kernels take pieces of any length).
+  const int64_t max_blk = max_piece_pages <= 0 ? INT64_MAX
+                          : page_size <= B     ? (int64_t)max_piece_pages * page_size / B
+                                               : (int64_t)(max_piece_pages - 1) * page_size / B;
   if (max_blk < 1)
     return fail(MLA_ERR_INVALID_ARG, "mla_decode_plan: max_piece_pages %d too small for page_size %d",
                 max_piece_pages, page_size);

@@ -111,16 +111,28 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
 #pragma unroll
     for (int ks = 0; ks < 18; ++ks) asm volatile("" ::"v"(qf[ks]));
 
-    // ---- page ids of the piece -> LDS
+    // ---- page ids of the piece -> LDS, one window of kMaxPieceIds pages at a time. t0 is a
+    // multiple of the 64-token plan block, so with pages under 32 tokens it is page aligned and
+    // a 32-token tile never straddles two windows (a window is a whole number of tiles); with
+    // larger pages a tile lies inside one page.
     const int pg0 = t0 >> p.log2_ps;
     const int npg = ((t1 - 1) >> p.log2_ps) - pg0 + 1;
-    __syncthreads();  // previous piece is done with s_ids and the ring
     const int32_t* pt_row = p.page_table + (int64_t)b * p.pt_stride + pg0;
-    for (int i = threadIdx.x; i < npg && i < kMaxPieceIds; i += NW * 64) {
-      const int id = pt_row[i];
-      s_ids[i] = min(max(id, 0), p.num_pages - 1);
-    }
-    __syncthreads();
+    int win = -1;  // window held by s_ids
+    auto tile_win = [&](int tile) { return (((t0 + tile * kTile) >> p.log2_ps) - pg0) / kMaxPieceIds; };
+    // Every wave calls this at the same point. The first barrier orders it after every read of the
+    // previous window (ids are read into registers when a tile is issued; DMAs already in flight do
+    // not read s_ids). Loading the ids waits for this wave's DMAs in flight (the vector-memory
+    // counter is in order): one drain of the ring per window.
+    auto stage_ids = [&](int wdx) {
+      __syncthreads();
+      const int base = wdx * kMaxPieceIds;
+      const int n = min(npg - base, kMaxPieceIds);
+      for (int i = threadIdx.x; i < n; i += NW * 64) s_ids[i] = min(max(pt_row[base + i], 0), p.num_pages - 1);
+      __syncthreads();
+      win = wdx;
+    };
+    stage_ids(0);  // also: the previous piece is done with s_ids and the ring
 
     const int ntiles = (t1 - t0 + kTile - 1) / kTile;
 
@@ -128,8 +140,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
       const int tstart = t0 + tile * kTile;
       const int tlim = t1 - 1 - tstart;  // last valid token of the tile (loads clamp to it)
       const uint32_t lds_stage = lds_ring + stage * kTileBytes;
+      const int id0 = pg0 + win * kMaxPieceIds;  // page of s_ids[0]
       if constexpr (kPageCoversTile) {
-        const int pid = __builtin_amdgcn_readfirstlane(s_ids[(tstart >> p.log2_ps) - pg0]);
+        const int pid = __builtin_amdgcn_readfirstlane(s_ids[(tstart >> p.log2_ps) - id0]);
         const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (tstart & ps_mask)) * row_bytes;
         if (tlim >= kTile - 1) {
 #pragma unroll
@@ -146,7 +159,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
         for (int k = 0; k < kDmaPerWave; ++k) {
           const int t = slot_token(k);
           const int tok = tstart + min(t, tlim);
-          const int pid = s_ids[(tok >> p.log2_ps) - pg0];
+          const int pid = s_ids[(tok >> p.log2_ps) - id0];
           const char* src = kv + ((int64_t)pid * (ps_mask + 1) + (tok & ps_mask)) * row_bytes + slot_chunk16(k, t);
           dma16_vaddr(src, lds_stage + (wave + k * NW) * 1024);
         }
@@ -158,9 +171,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     float l_run = 0.f;
     f32x4 O[32];
     for (int attempt = 0; attempt < 2; ++attempt) {
+      if (win != 0) stage_ids(0);  // a rerun restarts at the piece's first window
 #pragma unroll
       for (int s = 0; s < kStages - 1; ++s)
-        if (s < ntiles) issue(s, s);
+        if (s < ntiles) issue(s, s);  // the first kStages - 1 tiles lie in window 0
 #pragma unroll
       for (int i = 0; i < 32; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       l_run = 0.f;
@@ -172,7 +186,11 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
         else if (ahead == 1) wait_vmcnt<kDmaPerWave>();
         else wait_vmcnt<0>();
         __syncthreads();
-        if (it + kStages - 1 < ntiles) issue(it + kStages - 1, (it + kStages - 1) % kStages);
+        if (it + kStages - 1 < ntiles) {
+          const int nt = it + kStages - 1;
+          if (tile_win(nt) != win) stage_ids(tile_win(nt));  // uniform: same tile in every wave
+          issue(nt, nt % kStages);
+        }
 
         const MLA_LDS char* T = (const MLA_LDS char*)smem + (it % kStages) * kTileBytes;
 

@@ -22,7 +22,7 @@ with the attention math in libmla_amd.so:
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import List
+from typing import List, Tuple
 
 import numpy as np
 import torch
@@ -58,7 +58,8 @@ class MLAMetadata(BaseAttnMetadata):
     plan: torch.Tensor | None = None  # decode split-KV plan (device)
     num_slots: int = 0
     seqlens_k: List[int] | None = None  # host copy of cache_seqlens (prefill batches)
-    num_ctas: int = 0  # CTAs the decode plan was made for (0: the backend's default)
+    num_ctas: int = 0  # grid of the decode launch (the plan's CTA count)
+    workspace: Tuple[torch.Tensor, torch.Tensor] | None = None  # split-KV partials (decode)
 
     def get_last_indices(self, bs: int) -> torch.Tensor:
         return self.cu_seqlens_q[1 : 1 + bs] - 1
@@ -78,23 +79,30 @@ class MLAAttnBackend(BaseAttnBackend):
             dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
             num_ctas = lib.device_cu_count(dev_index)
         self.num_ctas = num_ctas
+        # every batch's tokens live in the pool, which bounds the grid a decode plan can need
+        self.pool_tokens = self.kvcache.num_pages * self.page_size
         self.capture: MLACaptureData | None = None
         self.capture_bs: List[int] = []
         self.max_graph_bs = 0
         self.capture_ctas = self.num_ctas
-        self.ws_o: torch.Tensor | None = None
-        self.ws_lse: torch.Tensor | None = None
+        # split-KV workspaces: eager batches use (and grow) their own; captured graphs keep theirs
+        # fixed from init_capture_graph, so an eager batch never resizes memory a graph points at
+        self.ws_eager: Tuple[torch.Tensor, torch.Tensor] | None = None
+        self.ws_graph: Tuple[torch.Tensor, torch.Tensor] | None = None
         self.last_lse: torch.Tensor | None = None  # natural-log LSE of the last forward
 
     # ------------------------------------------------------------------ workspace
-    def _ensure_workspace(self, slots: int) -> None:
-        have = 0 if self.ws_o is None else self.ws_o.shape[0]
-        if slots <= have:
-            return
-        assert self.capture is None, "captured graphs hold the workspace: it is sized once in init_capture_graph"
-        assert not torch.cuda.is_current_stream_capturing(), "workspace must be sized before capture"
-        self.ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.bfloat16, device=self.device)
-        self.ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
+    def _new_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+        assert not capturing, "decode workspaces are allocated outside capture"
+        ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.bfloat16, device=self.device)
+        ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
+        return ws_o, ws_lse
+
+    def _eager_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self.ws_eager is None or self.ws_eager[0].shape[0] < slots:
+            self.ws_eager = self._new_workspace(max(slots, 2 * self.num_ctas))
+        return self.ws_eager
 
     # ------------------------------------------------------------------ forward
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_id: int, batch: Batch) -> torch.Tensor:
@@ -106,9 +114,10 @@ class MLAAttnBackend(BaseAttnBackend):
         B, H, _ = q.shape
         out = torch.empty((B, H, self.config.kv_lora_rank), dtype=q.dtype, device=q.device)
         lse = torch.empty((B, H), dtype=torch.float32, device=q.device)
+        ws_o, ws_lse = metadata.workspace
         lib.mla_decode(
             q, self.kvcache.latent_cache(layer_id), metadata.page_table, metadata.cache_seqlens, metadata.plan,
-            metadata.num_ctas or self.num_ctas, self.ws_o, self.ws_lse, self.scale, out, lse,
+            metadata.num_ctas, ws_o, ws_lse, self.scale, out, lse,
         )
         self.last_lse = lse
         return out
@@ -160,18 +169,38 @@ class MLAAttnBackend(BaseAttnBackend):
                           dtype=torch.int32).to(dev, non_blocking=True)
         return k_tmp, v_tmp, pt
 
-    def _plan(self, seqlens_k: List[int], ctas: int):
-        """Split plan on ``ctas`` CTAs, doubling the count while the batch does not fit: with pages
-        under 32 tokens a piece holds at most MAX_PIECE_PAGES tokens' page ids, so a long batch can
-        need more pieces than compute units (the extra CTAs run as further rounds)."""
+    def _plan(self, seqlens_k: List[int], grid: int | None = None):
+        """Split plan on the smallest grid of ``num_ctas * 2^k`` CTAs that holds the batch (one CTA per
+        compute unit unless a CTA's range would pass the kernels' per-CTA limits of
+        ``MAX_CTA_BLOCKS`` blocks or ``MAX_CTA_REQUESTS`` requests; further CTAs run as further
+        rounds). With ``grid`` the plan is laid out for a launch of ``grid`` CTAs: the CTAs past the
+        planned ones get empty ranges. Returns ``(plan, slots, launch CTAs)``."""
+        ctas = self.num_ctas
+        limit = grid if grid is not None else max(self.num_ctas, self._grid_bound(sum(seqlens_k), len(seqlens_k)))
         while True:
             try:
                 plan_np, slots = lib.decode_plan(seqlens_k, self.page_size, ctas)
-                return plan_np, slots, ctas
+                break
             except lib.MLAKernelError as e:
-                if "cannot hold" not in str(e) or ctas >= 64 * self.num_ctas:
+                if "cannot hold" not in str(e) or ctas >= limit:
                     raise
                 ctas *= 2
+        assert slots <= 2 * ctas, "a CTA holds at most two pieces of split requests"
+        if grid is None or grid == ctas:
+            return plan_np, slots, ctas
+        return pad_plan(plan_np, ctas, grid, len(seqlens_k)), slots, grid
+
+    def _grid_bound(self, tokens: int, reqs: int) -> int:
+        """Smallest ``num_ctas * 2^k`` grid that holds any batch of ``reqs`` requests and ``tokens``
+        tokens in all: the planner closes a CTA only at ``MAX_CTA_BLOCKS`` blocks or
+        ``MAX_CTA_REQUESTS`` requests (pieces have no length limit), and each request rounds up by
+        less than one block."""
+        blocks = -(-tokens // lib.PLAN_BLOCK) + reqs
+        need = -(-blocks // lib.MAX_CTA_BLOCKS) + -(-reqs // (lib.MAX_CTA_REQUESTS - 1)) + 1
+        grid = self.num_ctas
+        while grid < need:
+            grid *= 2
+        return grid
 
     # ------------------------------------------------------------------ metadata
     def prepare_metadata(self, batch: Batch) -> None:
@@ -198,11 +227,17 @@ class MLAAttnBackend(BaseAttnBackend):
 
         is_decode = batch.is_decode
         plan_dev, slots, ctas = None, 0, 0
+        workspace = None
         if is_decode:
             assert max_seqlen_q == 1, "decode batches extend every request by one token"
-            graphed = self.capture is not None and padded_size <= self.max_graph_bs
-            plan_np, slots, ctas = self._plan(seqlens_k, self.capture_ctas if graphed else self.num_ctas)
-            self._ensure_workspace(max(slots, 1))
+            graphed = self.capture is not None and padded_size in self.capture_bs
+            if graphed:  # replayed: planned for the captured grid and workspace
+                plan_np, slots, ctas = self._plan(seqlens_k, self.capture_ctas)
+                workspace = self.ws_graph
+            else:
+                plan_np, slots, ctas = self._plan(seqlens_k)
+                workspace = self._eager_workspace(slots)
+            assert slots <= workspace[0].shape[0]
             plan_dev = torch.from_numpy(plan_np).pin_memory().to(device, non_blocking=True)
         batch.attn_metadata = MLAMetadata(
             cu_seqlens_k=cu_seqlens_k,
@@ -216,6 +251,7 @@ class MLAAttnBackend(BaseAttnBackend):
             num_slots=slots,
             seqlens_k=None if is_decode else seqlens_k,
             num_ctas=ctas if is_decode else 0,
+            workspace=workspace,
         )
 
     # ------------------------------------------------------------------ graph capture
@@ -223,12 +259,12 @@ class MLAAttnBackend(BaseAttnBackend):
         assert self.capture is None, "Capture already initialized."
         max_bs = max(bs_list)
         cols = -(-max_seq_len // self.page_size)
-        # the captured launch has a fixed grid: size it for the longest batch the graphs can see
-        _, _, self.capture_ctas = self._plan([max_seq_len] * max_bs, self.num_ctas)
+        # the captured launch has a fixed grid: the one the largest batch the graphs can replay needs,
+        # whose tokens are bounded by both the pool and max_bs * max_seq_len
+        self.capture_ctas = self._grid_bound(min(self.pool_tokens, max_bs * max_seq_len), max_bs)
         plan = torch.zeros((self.capture_ctas * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS,), dtype=torch.int32,
                            device=self.device)
-        # a plan never needs more partial slots than CTAs plus requests
-        self._ensure_workspace(self.capture_ctas + max_bs)
+        self.ws_graph = self._new_workspace(2 * self.capture_ctas)  # a plan needs at most 2 slots per CTA
         self.capture = MLACaptureData.create(max_bs, cols, self.device, plan=plan)
         self.max_graph_bs = max_bs
         self.capture_bs = sorted(bs_list)
@@ -236,7 +272,7 @@ class MLAAttnBackend(BaseAttnBackend):
     def prepare_for_capture(self, batch: Batch) -> None:
         assert (bs := batch.size) in self.capture_bs and self.capture is not None
         cap = self.capture
-        plan_np, _ = lib.decode_plan([r.device_len for r in batch.reqs], self.page_size, self.capture_ctas)
+        plan_np, _, _ = self._plan([r.device_len for r in batch.reqs], self.capture_ctas)
         n = plan_np.shape[0]
         cap.plan[:n].copy_(torch.from_numpy(plan_np))
         batch.attn_metadata = MLAMetadata(
@@ -248,8 +284,9 @@ class MLAAttnBackend(BaseAttnBackend):
             page_table=cap.page_table[:bs, :],
             is_decode=True,
             plan=cap.plan,
-            num_slots=self.ws_o.shape[0],
+            num_slots=self.ws_graph[0].shape[0],
             num_ctas=self.capture_ctas,
+            workspace=self.ws_graph,
         )
 
     def prepare_for_replay(self, batch: Batch) -> None:
@@ -263,6 +300,18 @@ class MLAAttnBackend(BaseAttnBackend):
         cap.page_table[:bs, :table_len].copy_(metadata.page_table)
         assert metadata.num_ctas == self.capture_ctas, "replayed batches are planned for the captured grid"
         cap.plan[: metadata.plan.numel()].copy_(metadata.plan)
+
+
+def pad_plan(plan: np.ndarray, ctas: int, grid: int, batch: int) -> np.ndarray:
+    """A plan made for ``ctas`` CTAs laid out for a launch of ``grid >= ctas`` CTAs: the extra CTAs
+    get the empty range ``(batch, 0, batch, 0)``; the request info is unchanged."""
+    assert grid >= ctas
+    out = np.empty(grid * lib.PLAN_CTA_INTS + batch * lib.PLAN_REQ_INTS, dtype=np.int32)
+    n = ctas * lib.PLAN_CTA_INTS
+    out[:n] = plan[:n]
+    out[n : grid * lib.PLAN_CTA_INTS] = np.tile(np.array([batch, 0, batch, 0], dtype=np.int32), grid - ctas)
+    out[grid * lib.PLAN_CTA_INTS :] = plan[n:]
+    return out
 
 
 def plan_pieces(plan: np.ndarray, num_ctas: int, seq_lens) -> List[tuple]:

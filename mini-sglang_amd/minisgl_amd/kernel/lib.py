@@ -69,7 +69,6 @@ ABI_VERSION = 5
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
-MAX_PIECE_PAGES = 1024
 MAX_CTA_BLOCKS = 1024
 MAX_CTA_REQUESTS = 128
 
@@ -163,9 +162,10 @@ def page_table_from_tokens(token_table, table_idx, max_seqlen_k: int, page_size:
 
 
 def decode_plan(
-    seq_lens, page_size: int, num_ctas: int, max_piece_pages: int = MAX_PIECE_PAGES
+    seq_lens, page_size: int, num_ctas: int, max_piece_pages: int = 0
 ) -> Tuple[np.ndarray, int]:
-    """Host split-KV plan: int32 ``[num_ctas*4 + B*3]`` (CTA ranges, then request info), slots."""
+    """Host split-KV plan: int32 ``[num_ctas*4 + B*3]`` (CTA ranges, then request info), slots.
+    ``max_piece_pages > 0`` caps the pages one piece touches (0: pieces of any length)."""
     lens = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.int32))
     B = int(lens.shape[0])
     plan = np.zeros(num_ctas * PLAN_CTA_INTS + B * PLAN_REQ_INTS, dtype=np.int32)

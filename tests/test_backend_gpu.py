@@ -78,16 +78,37 @@ def test_backend_decode_eager():
     assert torch.equal(md.get_last_indices(len(reqs)).cpu(), torch.arange(len(reqs), dtype=torch.int32))
 
 
+def _capture_decode(ctx, backend, tt, max_req, bs):
+    """Capture one decode forward at batch size ``bs`` (the dummy request fills the batch, as
+    python/minisgl/engine/graph.py:130-140 does); returns the graph and its static buffers."""
+    dummy = Req(table_idx=max_req, cached_len=0, device_len=1)
+    q_static = torch.zeros((bs, 64, 576), dtype=torch.bfloat16, device=DEV)
+    k_static = torch.zeros((bs, 576), dtype=torch.bfloat16, device=DEV)
+    loc_static = torch.full((bs,), int(tt[max_req, 0]), dtype=torch.int32, device=DEV)
+    cap = Batch(reqs=[dummy] * bs, phase="decode")
+    cap.padded_reqs = cap.reqs
+    cap.out_loc = loc_static
+    backend.prepare_for_capture(cap)
+    stream = torch.cuda.Stream()
+    with ctx.forward_batch(cap), torch.cuda.stream(stream):
+        backend.forward(q_static, k_static, None, 0, cap)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            o_static = backend.forward(q_static, k_static, None, 0, cap)
+    torch.cuda.synchronize()
+    return g, dummy, q_static, k_static, loc_static, o_static
+
+
 @pytest.mark.parametrize("page_size,graph_max_len", [(64, 4096), (1, 65536)])
 def test_backend_decode_graph_replay(page_size, graph_max_len):
-    """Capture and replay; at page size 1 the graphs' longest batch (8 x 65536 tokens) needs more
-    pieces than compute units, so the captured grid is 512 CTAs."""
+    """Capture and replay at page sizes 64 and 1. The captured grid is bounded by the pool's
+    tokens, so both run on one CTA per compute unit."""
     print(f"[graph replay] page_size={page_size}", flush=True)
     ctx, cfg, pool, backend, reqs, tt, max_req = _setup(page_size=page_size, seed=2)
     bs = 8
     dummy = Req(table_idx=max_req, cached_len=0, device_len=1)
     backend.init_capture_graph(max_seq_len=graph_max_len, bs_list=[bs])
-    assert backend.capture_ctas == (backend.num_ctas if page_size >= 32 else 2 * backend.num_ctas)
+    assert backend.capture_ctas == backend.num_ctas
     q_static = torch.zeros((bs, 64, 576), dtype=torch.bfloat16, device=DEV)
     k_static = torch.zeros((bs, 576), dtype=torch.bfloat16, device=DEV)
     loc_static = torch.full((bs,), int(tt[max_req, 0]), dtype=torch.int32, device=DEV)
@@ -189,10 +210,59 @@ def test_backend_prefill_with_prefix(page_size):
     assert torch.equal(md.get_last_indices(len(reqs)).cpu(), cu[1:] - 1)
 
 
+def test_backend_eager_batch_after_capture():
+    """A decode batch larger than every captured graph runs eagerly (python/minisgl/engine/
+    engine.py:194-196): 200 requests after graphs captured at batch size 8. It plans on its own
+    grid and workspace; the graph replayed afterwards still matches the oracle."""
+    gen = torch.Generator().manual_seed(11)
+    cached = torch.randint(63, 2048, (200,), generator=gen).tolist()
+    ctx, cfg, pool, backend, reqs, tt, max_req = _setup(page_size=64, max_req=200, max_seq_len=2112,
+                                                        cached=cached, seed=4)
+    bs = 8
+    backend.init_capture_graph(max_seq_len=2112, bs_list=[bs])
+    g, dummy, q_static, k_static, loc_static, o_static = _capture_decode(ctx, backend, tt, max_req, bs)
+    graph_ws = backend.ws_graph[0].data_ptr()
+
+    def run_eager():
+        batch = Batch(reqs=reqs, phase="decode")
+        batch.padded_reqs = reqs
+        batch.out_loc = torch.tensor([int(tt[r.table_idx, r.device_len - 1]) for r in reqs], dtype=torch.int32,
+                                     device=DEV)
+        backend.prepare_metadata(batch)
+        assert batch.attn_metadata.workspace[0].data_ptr() != graph_ws
+        q = torch.randn((len(reqs), 64, 576), generator=gen).to(torch.bfloat16).to(DEV)
+        k_new = pool.latent_cache(0).view(-1, 576)[batch.out_loc.long()].clone()
+        with ctx.forward_batch(batch):
+            o = backend.forward(q, k_new, None, 0, batch)
+        torch.cuda.synchronize()
+        print(f"[eager after capture] B={len(reqs)} ctas={batch.attn_metadata.num_ctas} "
+              f"slots={batch.attn_metadata.num_slots}", flush=True)
+        o_ref, lse_ref = _expected(pool, tt, reqs, q, 0, ctx.page_size)
+        torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+        torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
+
+    run_eager()
+    live = Batch(reqs=reqs[:bs], phase="decode")
+    live.padded_reqs = reqs[:bs]
+    live.out_loc = torch.tensor([int(tt[r.table_idx, r.device_len - 1]) for r in reqs[:bs]], dtype=torch.int32,
+                                device=DEV)
+    backend.prepare_metadata(live)
+    backend.prepare_for_replay(live)
+    q = torch.randn((bs, 64, 576), generator=gen).to(torch.bfloat16).to(DEV)
+    q_static.copy_(q)
+    k_static.copy_(pool.latent_cache(0).view(-1, 576)[live.out_loc.long()])
+    loc_static.copy_(live.out_loc)
+    g.replay()
+    torch.cuda.synchronize()
+    o_ref, _ = _expected(pool, tt, reqs[:bs], q, 0, ctx.page_size)
+    torch.testing.assert_close(o_static.float().cpu(), o_ref, **O_TOL)
+    run_eager()  # and eager again after the replay
+
+
 def test_backend_decode_page_size_one_kimi_batch():
-    """The reference's default page size (1) with the Kimi-K2 batch (B=64, L~U[1024,8192]): a piece
-    holds at most 1024 page ids, so the backend plans 512 CTAs (two rounds over the compute
-    units) rather than failing; output against the oracle."""
+    """The reference's default page size (1) with the Kimi-K2 batch (B=64, L~U[1024,8192]): one CTA
+    per compute unit, whose pieces (up to ~2600 tokens) pass the kernel's 1024-page-id LDS window,
+    so the kernel restages page ids mid-piece; output against the oracle."""
     from minisgl_amd.benchmark.inputs import make_decode_case
 
     reset_global_ctx()
@@ -215,7 +285,7 @@ def test_backend_decode_page_size_one_kimi_batch():
     batch.padded_reqs = reqs
     batch.out_loc = torch.tensor([int(tt[i, L - 1]) for i, L in enumerate(case.lens)], dtype=torch.int32, device=DEV)
     backend.prepare_metadata(batch)
-    assert batch.attn_metadata.num_ctas > backend.num_ctas
+    assert batch.attn_metadata.num_ctas == backend.num_ctas
     print(f"[backend ps=1] ctas={batch.attn_metadata.num_ctas}", flush=True)
     k_new = pool.latent_cache(0).view(-1, 576)[batch.out_loc.long()].clone()  # re-store the same rows
     with ctx.forward_batch(batch):

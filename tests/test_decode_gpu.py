@@ -275,3 +275,67 @@ def test_gather_rows_bit_exact(row_elems):
     ok = idx < 300
     assert torch.equal(out[ok.to(DEV)].view(torch.int16), cache[idx[ok].to(DEV)].view(torch.int16))
     assert torch.all(out[9] == 3.0)
+
+
+def _one_hot_targets(L, ps):
+    """Token positions whose rows a one-hot query must gather: the first and last token, page
+    edges, 32-token tile and 64-token plan-block edges, the 1024-page-id window edges, the last
+    token of a partial tile, and a few inside (at most 64, one rope dim each)."""
+    cand = [0, L - 1, ps - 1, ps, 2 * ps - 1, 31, 32, 63, 64, 65, 1023 * ps, 1024 * ps - 1, 1024 * ps,
+            (L - 1) // 32 * 32 - 1, L // 2, L // 3, 5 * L // 7]
+    out = []
+    for t in cand:
+        if 0 <= t < L and t not in out:
+            out.append(t)
+    return out[:64]
+
+
+@pytest.mark.parametrize("ps", [1, 16, 64])
+@pytest.mark.parametrize("num_ctas", [1, 7, 256])
+def test_decode_one_hot_gather_bit_exact(ps, num_ctas):
+    """A one-hot score makes every head's output the row it picks, bit for bit: target token k of
+    request b carries rope dim 512 + k = 64 (all other rope dims 0), head h's query is 64 in rope dim
+    h % n_b and 0 elsewhere, so its score is 64 * 64 / sqrt(192) = 295.6 for its target and 0 for
+    every other token (e^-295 vanishes in fp32). A wrong page, row, tile or window in the kernel's
+    gather shows up as a wrong row (the pattern of tests/kernel/test_index.py:52,91 in the
+    reference: bit-exact gathers). Splits across CTAs are merged with the same weights 1 and 0."""
+    H = 64
+    lens = [1, 31, 33, 64, 65, 1000, 2500, 5000] if ps == 1 else [1, 33, 64, 65, 1000, 2500, 5000, 20000]
+    print(f"[one-hot gather] ps={ps} ctas={num_ctas}", flush=True)
+    case = make_decode_case(len(lens), H, ps, lens=lens, seed=ps + num_ctas)
+    kv = case.kv_pool.clone()
+    kv[..., 512:] = 0
+    q = torch.zeros((len(lens), H, 576), dtype=torch.bfloat16)
+    flat = kv.view(-1, 576)
+    want = torch.empty((len(lens), H, 512), dtype=torch.bfloat16)
+    for b, L in enumerate(lens):
+        tg = _one_hot_targets(L, ps)
+        rows = [int(case.page_table[b, t // ps]) * ps + t % ps for t in tg]
+        for k, r in enumerate(rows):
+            flat[r, 512 + k] = 64.0
+        for h in range(H):
+            k = h % len(tg)
+            q[b, h, 512 + k] = 64.0
+            want[b, h] = flat[rows[k], :512]
+    out, lse, _ = run_decode(q.to(DEV), kv.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV), lens, ps,
+                             num_ctas)
+    got = out.to(torch.bfloat16)
+    bad = (got.view(torch.int16) != want.view(torch.int16)).any(-1)
+    assert not bad.any(), f"rows gathered wrongly at (request, head) {bad.nonzero()[:8].tolist()}"
+    s = 64.0 * 64.0 * R.DEFAULT_SCALE
+    torch.testing.assert_close(lse, torch.full_like(lse, s), atol=1e-3, rtol=0.0)
+
+
+@pytest.mark.parametrize("heads,ps", [(64, 1), (16, 1), (64, 2), (64, 16)])
+@pytest.mark.parametrize("num_ctas", [1, 3])
+def test_decode_long_pieces_small_pages(heads, ps, num_ctas):
+    """Pieces longer than the general kernel's LDS window of 1024 page ids (page sizes under 32):
+    the kernel restages the ids mid-piece; against the oracle."""
+    print(f"[long pieces] heads={heads} ps={ps} ctas={num_ctas}", flush=True)
+    lens = [5000, 3 * 1024 * ps + 17, 100, 2049]
+    case = make_decode_case(len(lens), heads, ps, lens=lens, seed=heads + ps)
+    plan_np, _ = lib.decode_plan(lens, ps, num_ctas)
+    from minisgl_amd.attention.mla import plan_pieces
+
+    assert max(t1 - t0 for *_, t0, t1 in plan_pieces(plan_np, num_ctas, lens)) > 1024 * ps
+    check_case(case, num_ctas)

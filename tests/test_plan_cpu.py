@@ -33,7 +33,7 @@ def _check(lens, ps, ctas):
         if req[b, 1] >= 2:
             used += list(range(req[b, 2], req[b, 2] + req[b, 1]))
     assert sorted(used) == list(range(slots))
-    assert slots <= ctas + B
+    assert slots <= ctas + B and slots <= 2 * ctas
     return plan, pieces
 
 
@@ -42,18 +42,26 @@ def _check(lens, ps, ctas):
 def test_plan_covers_every_token(ps, ctas):
     rng = np.random.default_rng(ps * 1000 + ctas)
     lens = rng.integers(0, 3000, size=13).tolist() + [0, 1, 64, 65]
-    # a piece may touch at most MAX_PIECE_PAGES pages, and every further piece of a
-    # request starts a new CTA, so the batch needs 1 + sum(pieces_b - 1) CTAs at least
-    max_blk = (lib.MAX_PIECE_PAGES * ps if ps <= lib.PLAN_BLOCK else (lib.MAX_PIECE_PAGES - 1) * ps) // lib.PLAN_BLOCK
-    max_blk = min(max_blk, lib.MAX_CTA_BLOCKS)
-    needed = 1 + sum(max(0, -(-(-(-L // lib.PLAN_BLOCK)) // max_blk) - 1) for L in lens)
-    # and one CTA holds at most MAX_CTA_BLOCKS blocks
+    # pieces have no length limit; one CTA holds at most MAX_CTA_BLOCKS blocks
     total_blocks = sum(-(-L // lib.PLAN_BLOCK) for L in lens)
-    if needed > ctas or -(-total_blocks // lib.MAX_CTA_BLOCKS) > ctas:
+    if -(-total_blocks // lib.MAX_CTA_BLOCKS) > ctas:
         with pytest.raises(lib.MLAKernelError):
             lib.decode_plan(lens, ps, ctas)
         return
     _check(lens, ps, ctas)
+
+
+@pytest.mark.parametrize("ps", [1, 16, 64, 128])
+def test_plan_piece_cap(ps):
+    """``max_piece_pages`` caps the pages a piece touches; every further piece of a request starts a
+    new CTA."""
+    lens = [5000, 3000, 64, 1]
+    plan, slots = lib.decode_plan(lens, ps, 64, max_piece_pages=128)
+    max_blk = (128 * ps if ps <= lib.PLAN_BLOCK else 127 * ps) // lib.PLAN_BLOCK
+    for _, b, t0, t1 in plan_pieces(plan, 64, lens):
+        assert -(-(t1 - t0) // lib.PLAN_BLOCK) <= max_blk
+    with pytest.raises(lib.MLAKernelError, match="cannot hold"):
+        lib.decode_plan([100000], ps, 2, max_piece_pages=128)
 
 
 def test_plan_is_balanced_for_kimi_decode():
@@ -66,40 +74,88 @@ def test_plan_is_balanced_for_kimi_decode():
     assert load.max() <= 1.15 * load.mean()
 
 
-def test_plan_long_context_and_piece_cap():
-    lens = [131072, 32768, 70000]
-    _check(lens, 64, 256)
-    # page size 1: a piece may touch at most 1024 pages (tokens)
-    plan, pieces = _check([5000, 3000], 1, 64)
-    assert max(t1 - t0 for _, _, t0, t1 in pieces) <= 1024
+def test_plan_long_context():
+    _check([131072, 32768, 70000], 64, 256)
+    # pieces of any length at page size 1 too: one CTA takes a whole 5000-token request
+    plan, pieces = _check([5000, 3000], 1, 1)
+    assert [(t0, t1) for _, _, t0, t1 in pieces] == [(0, 5000), (0, 3000)]
 
 
 def test_plan_rejects_impossible():
-    with pytest.raises(lib.MLAKernelError):
-        lib.decode_plan([100000], 1, 2)
+    # 200000 tokens = 3125 blocks > 2 * MAX_CTA_BLOCKS
+    with pytest.raises(lib.MLAKernelError, match="cannot hold"):
+        lib.decode_plan([200000], 1, 2)
+    # more than MAX_CTA_REQUESTS requests in one CTA
+    with pytest.raises(lib.MLAKernelError, match="cannot hold"):
+        lib.decode_plan([1] * (lib.MAX_CTA_REQUESTS + 1), 64, 1)
 
 
-def test_backend_plans_more_ctas_for_small_pages():
-    """With pages under 32 tokens a piece holds at most MAX_PIECE_PAGES tokens, so the Kimi-K2 batch
-    (336807 tokens) needs more pieces than 256 CTAs: the backend doubles the CTA count (the extra
-    CTAs run as further rounds) instead of failing; page size 64 keeps one CTA per compute unit."""
+def _backend(ps, pool_tokens=None, num_ctas=256):
     import torch
 
     from minisgl_amd.attention.mla import MLAAttnBackend
-    from minisgl_amd.benchmark.layer import decode_lens
     from minisgl_amd.config import MLAConfig
     from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
     from minisgl_amd.kvcache import create_kvcache_pool
 
+    reset_global_ctx()
+    ctx = Context(page_size=ps)
+    set_global_ctx(ctx)
+    ctx.kv_cache = create_kvcache_pool(MLAConfig(num_layers=1, num_heads=16), 4, ps, torch.bfloat16, "cpu")
+    be = MLAAttnBackend(MLAConfig(num_layers=1, num_heads=16), num_ctas=num_ctas)
+    if pool_tokens is not None:  # stands for a large pool without allocating it
+        be.pool_tokens = pool_tokens
+    reset_global_ctx()
+    return be
+
+
+@pytest.mark.parametrize("ps", [1, 64])
+def test_backend_plans_kimi_batch_on_one_round(ps):
+    """The Kimi-K2 batch (336807 tokens) fits one CTA per compute unit at any page size."""
+    from minisgl_amd.benchmark.layer import decode_lens
+
     lens = decode_lens()
-    with pytest.raises(lib.MLAKernelError, match="cannot hold"):
-        lib.decode_plan(lens, 1, 256)
-    for ps, want in ((1, 512), (64, 256)):
-        reset_global_ctx()
-        ctx = Context(page_size=ps)
-        set_global_ctx(ctx)
-        ctx.kv_cache = create_kvcache_pool(MLAConfig(num_layers=1), 4, ps, torch.bfloat16, "cpu")
-        be = MLAAttnBackend(MLAConfig(num_layers=1), num_ctas=256)
-        plan, slots, ctas = be._plan(lens, 256)
-        assert ctas == want and plan.shape[0] == ctas * lib.PLAN_CTA_INTS + len(lens) * lib.PLAN_REQ_INTS
-        reset_global_ctx()
+    be = _backend(ps)
+    plan, slots, ctas = be._plan(lens)
+    assert ctas == 256 and plan.shape[0] == ctas * lib.PLAN_CTA_INTS + len(lens) * lib.PLAN_REQ_INTS
+    assert slots <= 2 * ctas
+
+
+@pytest.mark.parametrize("ps", [1, 64])
+@pytest.mark.parametrize("max_bs", [160, 256])
+def test_capture_grid_is_bounded_by_the_pool(ps, max_bs):
+    """init_capture_graph at the reference's defaults (max_seq_len 131072, graph batch sizes up to
+    160 / 256, python/minisgl/engine/graph.py:58-62) sizes the captured grid from the pool's token
+    capacity, not max_bs * max_seq_len; replayed batches are planned on the smallest grid that
+    fits and padded with empty CTAs; eager batches larger than every graph (256 requests, the
+    reference's max_running_req) plan on their own workspace."""
+    be = _backend(ps, pool_tokens=2_000_000)
+    bs_list = [1, 2, 4] + list(range(8, max_bs + 1, 8))
+    be.init_capture_graph(max_seq_len=131072, bs_list=bs_list)
+    assert be.capture_ctas == 256
+    graph_ws = be.ws_graph[0]
+    assert graph_ws.shape[0] == 2 * be.capture_ctas
+    rng = np.random.default_rng(ps)
+    lens = rng.integers(1024, 8193, size=max_bs).tolist()
+    plan, slots, grid = be._plan(lens, be.capture_ctas)
+    assert grid == be.capture_ctas and slots <= graph_ws.shape[0]
+    assert plan.shape[0] == grid * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS
+    pieces = plan_pieces(plan, grid, lens)
+    assert sum(t1 - t0 for *_, t0, t1 in pieces) == sum(lens)
+    # a replayed batch with few tokens: the same grid, the CTAs past the planned ones empty
+    plan, slots, grid = be._plan([1] * 8, be.capture_ctas)
+    cta = plan[: grid * 4].reshape(grid, 4)
+    assert (cta[8:] == np.array([8, 0, 8, 0])).all()
+    # eager batches plan on their own grid and workspace, never on the graphs' one
+    big = rng.integers(1024, 8193, size=256).tolist()
+    plan, slots, ctas = be._plan(big)
+    ws = be._eager_workspace(slots)
+    assert ws[0].shape[0] >= slots and be.ws_graph[0] is graph_ws
+
+
+def test_capture_grid_grows_with_a_huge_pool():
+    """A pool whose batches can pass 256 CTAs x MAX_CTA_BLOCKS blocks doubles the captured grid."""
+    be = _backend(1, pool_tokens=40_000_000)
+    be.init_capture_graph(max_seq_len=131072, bs_list=[1, 160])
+    assert be.capture_ctas == 512  # 160 x 131072 = 21M tokens = 327680 blocks > 256 x 1024
+    assert be.capture_ctas * lib.MAX_CTA_BLOCKS * lib.PLAN_BLOCK >= 160 * 131072
