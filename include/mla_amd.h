@@ -14,7 +14,8 @@
  *     point synchronises or allocates device memory, so every launch is
  *     capturable into a HIP graph; the caller owns all buffers, including the
  *     split-KV workspace, as the reference's backends own theirs
- *     (python/minisgl/attention/fi.py:90-92).
+ *     (python/minisgl/attention/fi.py:90-92) -- except mla_decode_bf16_noalloc,
+ *     whose partials use the library's fixed device scratch instead.
  *   - bf16 tensors are raw uint16 bit patterns (bfloat16).
  */
 #ifndef MLA_AMD_H
@@ -159,6 +160,27 @@ int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                           const int32_t *plan, int32_t num_ctas, void *ws_o, float *ws_lse,
                           int32_t ws_slots, void *out, int64_t out_stride_b,
                           int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
+
+/*
+ * mla_decode_bf16 without a workspace argument: the split-KV partials go to a fixed scratch array
+ * inside the library (static device memory, one copy per GPU, held until the process ends) of
+ * MLA_NOALLOC_MAX_SLOT_HEADS slot-heads: 32 MiB of bf16 partials + 128 KiB of fp32 LSEs.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); it calls no
+ * allocating routine. num_slots is the plan's slot count (mla_decode_plan's *num_slots); a plan
+ * with num_slots * heads > MLA_NOALLOC_MAX_SLOT_HEADS is rejected with MLA_ERR_UNSUPPORTED. Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent streams)
+ * race. Nothing in the scratch must start at zero (the merge reads only slots the split kernel
+ * of the same call wrote).
+ */
+#define MLA_NOALLOC_MAX_SLOT_HEADS 32768
+int mla_decode_bf16_noalloc(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void *kv_pool, int64_t kv_row_stride, int32_t num_pages,
+                            int32_t page_size, const int32_t *page_table, int64_t pt_stride,
+                            const int32_t *seq_lens, int32_t batch, int32_t heads, float scale,
+                            const int32_t *plan, int32_t num_ctas, int32_t num_slots, void *out,
+                            int64_t out_stride_b, int64_t out_stride_h, float *lse,
+                            int64_t lse_stride_b, void *stream);
 
 /*
  * fp32 log-sum-exp merge of split-KV partials (bf16 ws_o, fp32 ws_lse; the merge step of

@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 5; }
+int mla_abi_version(void) { return 6; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -395,7 +395,30 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
                     const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
                     void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
                     void* stream) {
-  const char* who = "mla_decode_bf16";
+  return mla::decode_split_merge("mla_decode_bf16", q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages,
+                                 page_size, page_table, pt_stride, seq_lens, batch, heads, scale, plan, num_ctas,
+                                 ws_o, ws_lse, ws_slots, out, out_stride_b, out_stride_h, lse, lse_stride_b, stream);
+}
+
+}  // extern "C"
+
+namespace mla {
+
+int api_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
+                       int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
+                       int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
+                       const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots, void* out,
+                       int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
   if (batch == 0) return ok();
   if (int rc = check_head_groups(who, heads, q_stride_b, q_stride_h, out_stride_b, out_stride_h, lse, lse_stride_b))
@@ -408,13 +431,17 @@ int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
                                g.ws_lse, ws_slots, g.out, out_stride_b, out_stride_h, g.lse, lse_stride_b, &p))
       return rc;
     hipError_t e = mla::launch_decode(p, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_status(e, "mla_decode_bf16 split launch");
+    if (e != hipSuccess) return hip_status(e, "decode split launch");
     const mla::MergeParams m = merge_params(g.ws_o, g.ws_lse, ws_slots, plan + 4 * (int64_t)num_ctas, batch, g.heads,
                                             1, g.out, out_stride_b, out_stride_h, g.lse, lse_stride_b);
-    if (int rc = hip_status(mla::launch_merge(m, (hipStream_t)stream), "mla_decode_bf16 merge launch")) return rc;
+    if (int rc = hip_status(mla::launch_merge(m, (hipStream_t)stream), "decode merge launch")) return rc;
   }
   return ok();
 }
+
+}  // namespace mla
+
+extern "C" {
 
 int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
                          int32_t batch, int32_t heads, int32_t single_piece_final, void* out, int64_t out_stride_b,

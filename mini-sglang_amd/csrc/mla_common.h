@@ -96,6 +96,15 @@ struct PrefillParams {
   int64_t lse_stride_t;
 };
 
+// Host side of the decode entry points (mla_api.hip): the split kernel then the LSE merge over a
+// caller-given workspace, and the thread-local error message of mla_last_error().
+int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
+                       int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
+                       int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
+                       const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots, void* out,
+                       int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream);
+int api_error(int code, const char* fmt, ...);
+
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_decode_stream(const DecodeParams& p, hipStream_t stream);  // heads 64, pages >= 32

@@ -44,6 +44,11 @@ SIGNATURES = {
         [_vp, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i32,
          _vp, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp],
     ),
+    "mla_decode_bf16_noalloc": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i32, _i32,
+         _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
     "mla_decode_merge_f32": (
         ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _i64, _vp]
     ),
@@ -65,7 +70,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -216,6 +221,35 @@ def mla_decode(
             out.stride(1), _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
         ),
         "mla_decode_split_bf16" if split_only else "mla_decode_bf16",
+    )
+
+
+NOALLOC_MAX_SLOT_HEADS = 32768
+
+
+def mla_decode_noalloc(q, kv_pool, page_table, seq_lens, plan, num_ctas: int, num_slots: int, scale: float, out,
+                       lse=None, stream=None) -> None:
+    """``mla_decode`` with the split-KV partials in the library's fixed scratch (no workspace):
+    ``num_slots`` is the plan's slot count; calls that overlap on one GPU race."""
+    import torch
+
+    B, H, D = q.shape
+    assert D == 576 and kv_pool.shape[-1] == 576 and q.dtype == torch.bfloat16 and kv_pool.dtype == torch.bfloat16
+    assert q.stride(-1) == 1 and kv_pool.stride(-1) == 1
+    assert kv_pool.stride(0) == kv_pool.shape[1] * kv_pool.stride(1), "pool pages must be row-contiguous"
+    assert page_table.dtype == torch.int32 and seq_lens.dtype == torch.int32 and plan.dtype == torch.int32
+    assert out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.stride(-1) == 1
+    assert plan.numel() >= num_ctas * PLAN_CTA_INTS + B * PLAN_REQ_INTS
+    if lse is not None:
+        assert lse.dtype == torch.float32 and lse.shape == (B, H) and lse.stride(-1) == 1
+    check(
+        load_library().mla_decode_bf16_noalloc(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(kv_pool), kv_pool.stride(1),
+            kv_pool.shape[0], kv_pool.shape[1], _ptr(page_table), page_table.stride(0), _ptr(seq_lens), B, H,
+            float(scale), _ptr(plan), num_ctas, num_slots, _ptr(out), out.stride(0), out.stride(1), _ptr(lse),
+            0 if lse is None else lse.stride(0), _stream(stream),
+        ),
+        "mla_decode_bf16_noalloc",
     )
 
 
