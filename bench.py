@@ -283,7 +283,7 @@ def bench_decode(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "mla_decode_stream_kernel (split step)",
+            "kernel": "mla_decode_ws_kernel (split step)",
         },
     }
     if not args.no_cpu_baseline:
@@ -559,9 +559,12 @@ def bench_layer(args):
 
 def bench_peaks(args):
     """Measured peaks alone: the read-only HBM stream and the bf16 MFMA loop."""
+    import torch
+
     from minisgl_amd.benchmark import peaks
     from minisgl_amd.kernel import lib
 
+    torch.cuda.set_device(0)
     cus = lib.device_cu_count(0)
     return {"hbm_read": peaks.hbm_read(cus), "mfma_bf16": peaks.mfma_bf16(cus)}
 

@@ -43,7 +43,7 @@ enum {
 #define MLA_PLAN_CTA_INTS 4
 #define MLA_PLAN_REQ_INTS 3
 /* A decode plan gives one CTA at most this many plan blocks and requests. */
-#define MLA_PLAN_MAX_CTA_BLOCKS 1024
+#define MLA_PLAN_MAX_CTA_BLOCKS 512
 #define MLA_PLAN_MAX_CTA_REQUESTS 128
 
 /* Message for the last failed call on this thread ("" if none). */

@@ -234,8 +234,8 @@ int mla_decode_plan(const int32_t* seq_lens, int32_t batch, int32_t page_size, i
   int64_t lo = kPieceOverheadBlocks + 1, hi = total + kPieceOverheadBlocks + 1;
   if (plan_greedy(seq_lens, batch, hi, max_blk, num_ctas, false, nullptr, nullptr, nullptr) > num_ctas)
     return fail(MLA_ERR_UNSUPPORTED,
-                "mla_decode_plan: %d CTAs cannot hold the batch with pieces of at most %lld blocks", num_ctas,
-                (long long)max_blk);
+                "mla_decode_plan: %d CTAs cannot hold the batch (per CTA at most %d blocks and %d requests%s)",
+                num_ctas, mla::kMaxCtaBlocks, mla::kMaxCtaRequests, max_piece_pages > 0 ? ", capped pieces" : "");
   while (lo < hi) {
     const int64_t mid = lo + (hi - lo) / 2;
     if (plan_greedy(seq_lens, batch, mid, max_blk, num_ctas, false, nullptr, nullptr, nullptr) <= num_ctas)

@@ -107,7 +107,7 @@ int api_error(int code, const char* fmt, ...);
 
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
-hipError_t launch_decode_stream(const DecodeParams& p, hipStream_t stream);  // heads 64, pages >= 32
+hipError_t launch_decode_ws(const DecodeParams& p, hipStream_t stream);      // heads 64, pages >= 32
 hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
 hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
                              const void* indices, int index_bits, int64_t rows, int64_t row_bytes,

@@ -42,6 +42,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void dma16_saddr(const char* base, uint32_t voff, uint32_t lds_base) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
 }
+// The same with the non-temporal hint: for data read once (streamed KV rows), so the caches keep
+// the lines that are reused.
+__device__ __forceinline__ void dma16_saddr_nt(const char* base, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(base), "{m0}"(lds_base) : "memory");
+}
 __device__ __forceinline__ void dma16_vaddr(const char* addr, uint32_t lds_base) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds_base) : "memory");
 }

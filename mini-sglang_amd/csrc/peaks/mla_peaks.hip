@@ -37,6 +37,7 @@ __global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* __restrict__
 
 // Global -> LDS DMA stream (the staging path of the decode kernel): each wave moves 1 KiB per
 // instruction into a 4-stage LDS ring; one XOR of the ring per stage keeps the loads live.
+template <bool kNonTemporal>
 __global__ __launch_bounds__(256) void hbm_read_lds_kernel(const char* __restrict__ src, int64_t nbytes,
                                                            uint32_t* __restrict__ sink) {
   constexpr int kStage = 32768;  // bytes per CTA per stage
@@ -53,7 +54,10 @@ __global__ __launch_bounds__(256) void hbm_read_lds_kernel(const char* __restric
       const int chunk = wave + 4 * k;
       const char* a = src + base + chunk * 1024 + lane * 16;
       const uint32_t l = lds0 + st * kStage + chunk * 1024;
-      mla::dma16_vaddr(a, l);
+      if constexpr (kNonTemporal)
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(a), "{m0}"(l) : "memory");
+      else
+        mla::dma16_vaddr(a, l);
     }
     if (n >= 2) {  // consume the stage issued two rounds ago; the barrier waits on LDS only
       mla::wait_vmcnt<16>();
@@ -98,7 +102,7 @@ extern "C" {
 
 // Stream `nbytes` (a multiple of 16) of `src` once on `ctas` CTAs of 256 threads. variant: 0-2 =
 // 16-byte vector loads with 4 / 8 / 16 in flight per thread, 3 = 8 in flight, non-temporal;
-// 4 = global->LDS DMA (nbytes a multiple of 32 KiB). `sink` holds ctas * 256 uint32.
+// 4 = global->LDS DMA, 5 = the same with the non-temporal hint (nbytes a multiple of 32 KiB). `sink` holds ctas * 256 uint32.
 int mla_peaks_hbm_read(const void* src, int64_t nbytes, int32_t ctas, int32_t variant, void* sink, void* stream) {
   if (src == nullptr || sink == nullptr || nbytes <= 0 || nbytes % 16 != 0 || ctas < 1) return 1;
   const hipStream_t s = (hipStream_t)stream;
@@ -111,8 +115,14 @@ int mla_peaks_hbm_read(const void* src, int64_t nbytes, int32_t ctas, int32_t va
     case 2: hipLaunchKernelGGL((hbm_read_kernel<16, false>), dim3(ctas), dim3(256), 0, s, p, n16, out); break;
     case 3: hipLaunchKernelGGL((hbm_read_kernel<8, true>), dim3(ctas), dim3(256), 0, s, p, n16, out); break;
     case 4:
+    case 5:
       if (nbytes % 32768 != 0) return 1;
-      hipLaunchKernelGGL(hbm_read_lds_kernel, dim3(ctas), dim3(256), 0, s, static_cast<const char*>(src), nbytes, out);
+      if (variant == 4)
+        hipLaunchKernelGGL(hbm_read_lds_kernel<false>, dim3(ctas), dim3(256), 0, s, static_cast<const char*>(src),
+                           nbytes, out);
+      else
+        hipLaunchKernelGGL(hbm_read_lds_kernel<true>, dim3(ctas), dim3(256), 0, s, static_cast<const char*>(src),
+                           nbytes, out);
       break;
     default: return 1;
   }

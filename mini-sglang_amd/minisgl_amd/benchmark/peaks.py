@@ -12,7 +12,8 @@ PEAKS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmla_pe
 HBM_SPEC_TBPS = 8.0
 MFMA_BF16_SPEC_TFLOPS = 2500.0
 READ_VARIANTS = {0: "vector loads, 4 in flight", 1: "vector loads, 8 in flight", 2: "vector loads, 16 in flight",
-                 3: "vector loads, 8 in flight, non-temporal", 4: "global->LDS DMA, 4-stage ring"}
+                 3: "vector loads, 8 in flight, non-temporal", 4: "global->LDS DMA, 4-stage ring",
+                5: "global->LDS DMA, 4-stage ring, non-temporal"}
 
 
 @functools.lru_cache(maxsize=None)
@@ -54,7 +55,7 @@ def hbm_read(cu_count: int, gib: int = 4, reps: int = 3) -> dict:
     stream = torch.cuda.current_stream()
     results = []
     for variant in READ_VARIANTS:
-        for mult in ((1,) if variant == 4 else (1, 2, 4, 8)):
+        for mult in ((1,) if variant >= 4 else (1, 2, 4, 8)):
             ctas = cu_count * mult
             sink = torch.empty(ctas * 256, dtype=torch.int32, device="cuda")
 

@@ -74,7 +74,7 @@ ABI_VERSION = 6
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
-MAX_CTA_BLOCKS = 1024
+MAX_CTA_BLOCKS = 512
 MAX_CTA_REQUESTS = 128
 
 

@@ -157,5 +157,10 @@ def test_capture_grid_grows_with_a_huge_pool():
     """A pool whose batches can pass 256 CTAs x MAX_CTA_BLOCKS blocks doubles the captured grid."""
     be = _backend(1, pool_tokens=40_000_000)
     be.init_capture_graph(max_seq_len=131072, bs_list=[1, 160])
-    assert be.capture_ctas == 512  # 160 x 131072 = 21M tokens = 327680 blocks > 256 x 1024
+    # 160 x 131072 = 21M tokens = 327680 blocks: more than 256 (and 512) CTAs x MAX_CTA_BLOCKS
+    assert be.capture_ctas == 1024 and lib.MAX_CTA_BLOCKS == 512
     assert be.capture_ctas * lib.MAX_CTA_BLOCKS * lib.PLAN_BLOCK >= 160 * 131072
+    rng = np.random.default_rng(7)
+    lens = rng.integers(100_000, 131_073, size=160).tolist()
+    plan, slots, grid = be._plan(lens, be.capture_ctas)
+    assert grid == 1024 and sum(t1 - t0 for *_, t0, t1 in plan_pieces(plan, grid, lens)) == sum(lens)
