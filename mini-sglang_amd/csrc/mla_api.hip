@@ -53,7 +53,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 6; }
+int mla_abi_version(void) { return 7; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -263,7 +263,7 @@ static int check_out(const void* out, int64_t sb, int64_t sh, const float* lse, 
 static int decode_params(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          const void* kv_pool, int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
                          const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens, int32_t batch,
-                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, void* ws_o,
+                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, float* ws_o,
                          float* ws_lse, int32_t ws_slots, void* out, int64_t out_stride_b, int64_t out_stride_h,
                          float* lse, int64_t lse_stride_b, mla::DecodeParams* p) {
   if (heads < 1 || heads > 64) return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be in [1, 64], got %d", who, heads);
@@ -299,7 +299,7 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
   p->scale_log2 = scale * 1.4426950408889634f;
   p->plan = plan;
   p->num_ctas = num_ctas;
-  p->ws_o = static_cast<__bf16*>(ws_o);
+  p->ws_o = ws_o;
   p->ws_lse = ws_lse;
   p->ws_slots = ws_slots;
   p->out = static_cast<__bf16*>(out);
@@ -310,12 +310,12 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
   return MLA_OK;
 }
 
-static mla::MergeParams merge_params(const void* ws_o, const float* ws_lse, int32_t ws_slots,
+static mla::MergeParams merge_params(const float* ws_o, const float* ws_lse, int32_t ws_slots,
                                      const int32_t* req_info, int32_t batch, int32_t heads, int32_t skip_single,
                                      void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                                      int64_t lse_stride_b) {
   mla::MergeParams m;
-  m.ws_o = static_cast<const __bf16*>(ws_o);
+  m.ws_o = ws_o;
   m.ws_lse = ws_lse;
   m.ws_slots = ws_slots;
   m.req_info = req_info;
@@ -338,19 +338,19 @@ constexpr int32_t kMaxHeads = 1024;
 
 struct HeadGroup {
   const void* q;
-  void* ws_o;
+  float* ws_o;
   float* ws_lse;
   void* out;
   float* lse;
   int32_t heads;
 };
 
-static HeadGroup head_group(int32_t h0, int32_t heads, int32_t ws_slots, const void* q, int64_t q_stride_h, void* ws_o,
+static HeadGroup head_group(int32_t h0, int32_t heads, int32_t ws_slots, const void* q, int64_t q_stride_h, float* ws_o,
                             float* ws_lse, void* out, int64_t out_stride_h, float* lse) {
   HeadGroup g;
   g.heads = heads - h0 < kHeadGroup ? heads - h0 : kHeadGroup;
   g.q = q == nullptr ? nullptr : static_cast<const __bf16*>(q) + (int64_t)h0 * q_stride_h;
-  g.ws_o = ws_o == nullptr ? nullptr : static_cast<__bf16*>(ws_o) + (int64_t)ws_slots * h0 * MLA_V_DIM;
+  g.ws_o = ws_o == nullptr ? nullptr : ws_o + (int64_t)ws_slots * h0 * MLA_V_DIM;
   g.ws_lse = ws_lse == nullptr ? nullptr : ws_lse + (int64_t)ws_slots * h0;
   g.out = static_cast<__bf16*>(out) + (int64_t)h0 * out_stride_h;
   g.lse = lse == nullptr ? nullptr : lse + h0;
@@ -369,7 +369,7 @@ static int check_head_groups(const char* who, int32_t heads, int64_t q_stride_b,
 int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                           int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                           int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                          const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
+                          const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
                           void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                           int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_split_bf16";
@@ -392,7 +392,7 @@ int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                     int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                     int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                    const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
+                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
                     void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
                     void* stream) {
   return mla::decode_split_merge("mla_decode_bf16", q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages,
@@ -417,7 +417,7 @@ int api_error(int code, const char* fmt, ...) {
 int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                        int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                        int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                       const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots, void* out,
+                       const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots, void* out,
                        int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
   if (batch == 0) return ok();
@@ -443,7 +443,7 @@ int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64
 
 extern "C" {
 
-int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
+int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
                          int32_t batch, int32_t heads, int32_t single_piece_final, void* out, int64_t out_stride_b,
                          int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_merge_f32";
@@ -454,7 +454,7 @@ int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots
   if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
   if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
   for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {  // the workspace holds one [slots, group, 512] block per group
-    const HeadGroup g = head_group(h0, heads, ws_slots, nullptr, 0, const_cast<void*>(ws_o),
+    const HeadGroup g = head_group(h0, heads, ws_slots, nullptr, 0, const_cast<float*>(ws_o),
                                    const_cast<float*>(ws_lse), out, out_stride_h, lse);
     const mla::MergeParams m = merge_params(g.ws_o, g.ws_lse, ws_slots, req_info, batch, g.heads,
                                             single_piece_final ? 1 : 0, g.out, out_stride_b, out_stride_h, g.lse,

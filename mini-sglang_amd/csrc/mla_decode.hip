@@ -307,23 +307,19 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_decode_kernel(const DecodePara
     } else {
       const int slot = slot_base + (w - first_cta);
       if (slot >= 0 && slot < p.ws_slots) {
-        __bf16* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 4 * g;
+        float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 32; ++db) {
-          u32x2 v;
-          v[0] = pack_bf16x2(O[db][0] * inv, O[db][1] * inv);
-          v[1] = pack_bf16x2(O[db][2] * inv, O[db][3] * inv);
-          *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
-        }
+        for (int db = 0; db < 32; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[db] * inv;
         if (g == 0) p.ws_lse[(int64_t)slot * p.heads + h] = lse_nat;
       }
     }
   }
 }
 
-// One wave per (request, head): lane holds dims 8*lane .. +8.
-// One wave per (request, head): lane i holds piece i's LSE (64 pieces per pass);
-// the partials are read 8 pieces at a time with all loads in flight together.
+// One wave per (request, head): lane l holds value dims 8l .. 8l+7 of the fp32 partials and the LSE
+// of piece l (of each group of 64 pieces). The first 8 pieces' partials are requested before the
+// LSE reduction, so a request of up to 8 pieces costs one memory round trip; later pieces are read
+// 8 at a time with all loads in flight together.
 constexpr int kMergeBatch = 8;
 
 __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
@@ -339,14 +335,32 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
     const int s = base + i;
     return (i < n && s >= 0 && s < p.ws_slots) ? p.ws_lse[(int64_t)s * p.heads + h] : -INFINITY;
   };
+  // Loads are unconditional (branch-free): the slot is clamped into the workspace, and a piece
+  // past n or outside it has LSE -inf, so its data is selected away in the sum.
+  const bool have = n > 0 && p.ws_slots > 0;
+  auto load = [&](int i, f32x4& lo, f32x4& hi) {
+    const int s = min(max(base + min(i, n - 1), 0), p.ws_slots - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
+    lo = src[0];
+    hi = src[1];
+  };
 
-  float mx = -INFINITY;
-  for (int i = lane; i < n; i += 64) mx = fmaxf(mx, piece_lse(i));
+  f32x4 a[kMergeBatch], bq[kMergeBatch];
+  if (have) {
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) load(u, a[u], bq[u]);
+  }
+  const float lse0 = piece_lse(lane);
+
+  float mx = lse0;
+  for (int i = lane + 64; i < n; i += 64) mx = fmaxf(mx, piece_lse(i));
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   float sum = 0.f;
-  if (mx > -INFINITY)
-    for (int i = lane; i < n; i += 64) sum += expf(piece_lse(i) - mx);
+  if (mx > -INFINITY) {
+    sum = lse0 > -INFINITY ? expf(lse0 - mx) : 0.f;
+    for (int i = lane + 64; i < n; i += 64) sum += expf(piece_lse(i) - mx);
+  }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
   const bool any = mx > -INFINITY && sum > 0.f;
@@ -354,35 +368,25 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const MergeParams p) {
 
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (any) {
+#pragma unroll 1
     for (int i0 = 0; i0 < n; i0 += 64) {
-      const float my_lse = piece_lse(i0 + lane);  // lane u: piece i0 + u
+      const float my_lse = i0 == 0 ? lse0 : piece_lse(i0 + lane);  // lane u: piece i0 + u
       const int cnt = min(64, n - i0);
+#pragma unroll 1
       for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
-        f32x4 a[kMergeBatch], bq[kMergeBatch];
+        if (i0 + u0 > 0) {
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
-          const int s = base + i0 + u0 + u;
-          a[u] = bq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (u0 + u < cnt && s >= 0 && s < p.ws_slots) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(p.ws_o +
-                                                            ((int64_t)s * p.heads + h) * kVDim + 8 * lane);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              a[u][2 * j] = __uint_as_float(w[j] << 16);
-              a[u][2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-              bq[u][2 * j] = __uint_as_float(w[2 + j] << 16);
-              bq[u][2 * j + 1] = __uint_as_float(w[2 + j] & 0xffff0000u);
-            }
-          }
+          for (int u = 0; u < kMergeBatch; ++u) load(i0 + u0 + u, a[u], bq[u]);
         }
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
           const float l_u = __shfl(my_lse, u0 + u);
-          const float wgt = (u0 + u < cnt && l_u > -INFINITY) ? expf(l_u - lse) : 0.f;
+          const bool ok = u0 + u < cnt && l_u > -INFINITY;
+          const float wgt = ok ? expf(l_u - lse) : 0.f;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            acc[j] += wgt * a[u][j];
-            acc[4 + j] += wgt * bq[u][j];
+            acc[j] = ok ? fmaf(wgt, a[u][j], acc[j]) : acc[j];
+            acc[4 + j] = ok ? fmaf(wgt, bq[u][j], acc[4 + j]) : acc[4 + j];
           }
         }
       }

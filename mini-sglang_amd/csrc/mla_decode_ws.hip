@@ -18,7 +18,8 @@
 //    Every K row is read from LDS by two waves, every V row by one. A SIMD holds one wave of each
 //    role, so one role's LDS and barrier waits are covered by the other's MFMAs. One barrier per step
 //    (two at a piece's first KV tile): step j scores tile j and accumulates tile j - 1; the output
-//    waves normalise and store a piece and write its LSE.
+//    waves normalise and store a piece (bf16 output, or the fp32 partial of a split request) and
+//    write its LSE.
 //  * No accumulator rescaling: exponents are taken against the piece's first-tile max; a piece whose
 //    later scores exceed it by 2^64 is rerun with its exact max (the vote is taken at the step after
 //    the piece's last tile, before any wave touches the next tile).
@@ -35,8 +36,8 @@ namespace {
 constexpr int kWWaves = 8;
 constexpr int kWAhead = 2;         // stream tiles in flight beyond the one being scored
 // A tile's 36 wave-wide DMA loads ("parts") are split between the roles: score wave r issues parts
-// r + 4k (k < kWScoreParts), output wave r parts 4 kWScoreParts + r + 4k (k < kWOutParts); output
-// waves; a role issues its parts after its step's work (instead of right after the step's barrier)
+// r + 4k (k < kWScoreParts), output wave r parts 4 kWScoreParts + r + 4k (k < kWOutParts); a role
+// issues its parts after its step's work (instead of right after the step's barrier)
 // when its Late flag is set.
 constexpr int kWScoreParts = 0;
 constexpr int kWOutParts = 9;
@@ -471,14 +472,19 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
             const int h = 16 * hq + c;
             const float l = s_l[0][h] + s_l[1][h];
             const float inv = l > 0.f ? 1.f / l : 0.f;
-            __bf16* orow = to_ws ? p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 128 * role + 4 * g
-                                 : p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 128 * role + 4 * g;
+            if (to_ws) {  // fp32 partial for the merge
+              float* orow = p.ws_o + ((int64_t)slot * p.heads + h) * kVDim + 128 * role + 4 * g;
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-              u32x2 v;
-              v[0] = pack_bf16x2(O[hq][db][0] * inv, O[hq][db][1] * inv);
-              v[1] = pack_bf16x2(O[hq][db][2] * inv, O[hq][db][3] * inv);
-              *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+              for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db) = O[hq][db] * inv;
+            } else {
+              __bf16* orow = p.out + (int64_t)b * p.out_stride_b + (int64_t)h * p.out_stride_h + 128 * role + 4 * g;
+#pragma unroll
+              for (int db = 0; db < 8; ++db) {
+                u32x2 v;
+                v[0] = pack_bf16x2(O[hq][db][0] * inv, O[hq][db][1] * inv);
+                v[1] = pack_bf16x2(O[hq][db][2] * inv, O[hq][db][3] * inv);
+                *reinterpret_cast<u32x2*>(orow + 16 * db) = v;
+              }
             }
           }
           ops += 32;

@@ -14,7 +14,7 @@
 namespace {
 
 constexpr int64_t kMaxSlotHeads = MLA_NOALLOC_MAX_SLOT_HEADS;
-constexpr int64_t kPartialBytes = kMaxSlotHeads * MLA_V_DIM * 2;  // bf16 partial outputs
+constexpr int64_t kPartialBytes = kMaxSlotHeads * MLA_V_DIM * 4;  // fp32 partial outputs
 constexpr int64_t kScratchBytes = kPartialBytes + kMaxSlotHeads * 4;  // + fp32 LSEs
 static_assert(kPartialBytes % 256 == 0, "LSE block alignment");
 
@@ -65,7 +65,7 @@ int mla_decode_bf16_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_
   void* base = nullptr;
   if (int rc = scratch_address(&base)) return rc;
   // every slot the merge reads is written by the split kernel of the same call: nothing to clear
-  void* ws_o = base;
+  float* ws_o = static_cast<float*>(base);
   float* ws_lse = reinterpret_cast<float*>(static_cast<char*>(base) + kPartialBytes);
   return mla::decode_split_merge(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size,
                                  page_table, pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse,

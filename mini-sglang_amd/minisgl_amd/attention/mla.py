@@ -95,7 +95,7 @@ class MLAAttnBackend(BaseAttnBackend):
     def _new_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
         capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
         assert not capturing, "decode workspaces are allocated outside capture"
-        ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.bfloat16, device=self.device)
+        ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.float32, device=self.device)
         ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
         return ws_o, ws_lse
 

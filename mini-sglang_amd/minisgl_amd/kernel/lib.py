@@ -70,7 +70,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -209,7 +209,7 @@ def mla_decode(
     ws_slots = 0 if ws_o is None else ws_o.shape[0]
     if ws_o is not None:
         assert ws_o.shape[1:] == (H, 512) and ws_lse.shape[:2] == (ws_slots, H)
-        assert ws_o.dtype == torch.bfloat16 and ws_lse.dtype == torch.float32
+        assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32
     if lse is not None:
         assert lse.dtype == torch.float32 and lse.shape == (B, H) and lse.stride(-1) == 1
     fn = load_library().mla_decode_split_bf16 if split_only else load_library().mla_decode_bf16
@@ -254,10 +254,10 @@ def mla_decode_noalloc(q, kv_pool, page_table, seq_lens, plan, num_ctas: int, nu
 
 
 def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None, single_piece_final: bool = False) -> None:
-    """fp32 LSE merge of partials ``ws_o [S, H, 512]`` (bf16) / ``ws_lse [S, H]`` (fp32) per ``req_info``."""
+    """fp32 LSE merge of partials ``ws_o [S, H, 512]`` / ``ws_lse [S, H]`` (both fp32) per ``req_info``."""
     import torch
 
-    assert ws_o.dtype == torch.bfloat16 and ws_lse.dtype == torch.float32, "ws_o bf16, ws_lse fp32"
+    assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32, "ws_o and ws_lse are fp32"
     B, H = out.shape[0], out.shape[1]
     check(
         load_library().mla_decode_merge_f32(

@@ -21,7 +21,7 @@ def _both(case, num_ctas):
     plan_np, slots = lib.decode_plan(case.lens, case.page_size, num_ctas)
     plan = torch.from_numpy(plan_np).to(DEV)
     q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
-    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.bfloat16, device=DEV)
+    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=DEV)
     ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=DEV)
     out_a = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
     lse_a = torch.full((B, H), float("nan"), dtype=torch.float32, device=DEV)
