@@ -70,15 +70,25 @@ int mla_store_rows(void *cache, int64_t cache_rows, int64_t cache_row_stride_byt
                    int32_t index_bits, int64_t num_rows, int64_t row_bytes, void *stream);
 
 /*
- * out[i, :] = cache[indices[i], :] for i < num_rows (int64 indices; rows of row_bytes, a multiple of
- * 16; strides in bytes). The inverse of mla_store_rows; rows whose index lies outside
- * [0, cache_rows) are left untouched. Used to gather a request's per-head K/V rows from pools
- * with pages under 64 tokens into the 64-token pages the prefill kernel reads (the gather the
- * FA backend's paged reads do, python/minisgl/attention/fa.py:157-182).
+ * Latent rows of every key of a prefill batch into 64-row scratch pages, the input of the per-head
+ * decompression that lets chunked prefill run over a latent-only pool (the caller role of
+ * python/minisgl/layers/attention.py:47-57 for MLA; the pool it reads replaces
+ * python/minisgl/kvcache/mha_pool.py:10-68). Key j < seq_lens_k[b] of request b, pool row
+ * page_table[b, j / page_size] * page_size + j % page_size of kv_pool ([num_pages, page_size, 576],
+ * row stride kv_row_stride; page ids clamped into [0, num_pages)), goes to scratch row
+ * r = 64 * seg_first[b] + j: its 512 latent dims to c_out[r, :] (row stride c_row_stride) and its 64
+ * rope dims to rope_out[r, :] (row stride rope_row_stride); rows r >= out_rows are not written.
+ * seg_page_table[b, i] = seg_first[b] + i for i < ceil(seq_lens_k[b] / 64) (row stride
+ * seg_pt_stride >= max_seg_pages), so the scratch rows are 64-token pages under that table.
+ * max_seg_pages >= ceil(seq_lens_k[b] / 64) for every b (keys past it are not copied). Any
+ * power-of-two page_size (1 included); bit-exact.
  */
-int mla_gather_rows(void *out, int64_t out_row_stride_bytes, const void *cache, int64_t cache_rows,
-                    int64_t cache_row_stride_bytes, const int64_t *indices, int64_t num_rows, int64_t row_bytes,
-                    void *stream);
+int mla_prefill_gather_bf16(const void *kv_pool, int64_t kv_row_stride, int32_t num_pages,
+                            int32_t page_size, const int32_t *page_table, int64_t pt_stride,
+                            const int32_t *seq_lens_k, const int32_t *seg_first, int32_t batch,
+                            int32_t max_seg_pages, void *c_out, int64_t c_row_stride, void *rope_out,
+                            int64_t rope_row_stride, int64_t out_rows, int32_t *seg_page_table,
+                            int64_t seg_pt_stride, void *stream);
 
 /*
  * Token table -> page table, bit-exact:
@@ -224,6 +234,30 @@ int mla_prefill_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, cons
                      int32_t batch, int32_t total_q, int32_t heads, float scale, void *out,
                      int64_t out_stride_t, int64_t out_stride_h, float *lse, int64_t lse_stride_t,
                      void *stream);
+
+/*
+ * mla_prefill_bf16 with the K and V rows anywhere (same semantics, same fixed kernel): the K row of
+ * (token row r = page * page_size + offset, head h) is 128 nope dims at
+ * k_nope + r * k_row_stride + h * k_head_stride followed, somewhere after them, by 64 rope dims at
+ * k_rope + r * k_row_stride + h * k_rope_head_stride (k_rope_head_stride 0: one rope row per token,
+ * shared by all heads, as MLA's k_pe is); the V row is 128 dims at v + r * v_row_stride +
+ * h * v_head_stride. The rope dims of every head must lie 256 bytes to 2 GiB after its nope dims
+ * (else MLA_ERR_UNSUPPORTED). mla_prefill_bf16 is the case k_head_stride = k_rope_head_stride =
+ * 192, k_rope = k_pool + 128, v_head_stride = 128. The layout of the latent decompression
+ * (mla_prefill_gather_bf16, then [k_nope | v] = c W_kvb^T per head) is
+ * row = [head 0: k_nope 128 | v 128, head 1: ..., rope 64]: k_head_stride = v_head_stride = 256,
+ * k_rope = k_nope + 256 * heads, k_rope_head_stride = 0, v = k_nope + 128. No counterpart in the
+ * reference (its FA call reads one per-head K/V layout).
+ */
+int mla_prefill_strided_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h,
+                             const void *k_nope, int64_t k_row_stride, int64_t k_head_stride,
+                             const void *k_rope, int64_t k_rope_head_stride, const void *v,
+                             int64_t v_row_stride, int64_t v_head_stride, int32_t num_pages,
+                             int32_t page_size, const int32_t *page_table, int64_t pt_stride,
+                             const int32_t *cu_seqlens_q, const int32_t *seq_lens_k, int32_t batch,
+                             int32_t total_q, int32_t heads, float scale, void *out,
+                             int64_t out_stride_t, int64_t out_stride_h, float *lse,
+                             int64_t lse_stride_t, void *stream);
 
 /*
  * The elementwise steps of the DeepSeek-V3 / Kimi-K2 MLA layer around the attention calls

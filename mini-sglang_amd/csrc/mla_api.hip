@@ -6,6 +6,8 @@
 
 #include <limits.h>
 
+#include <algorithm>
+
 #include <string>
 
 #include "../../include/mla_amd.h"
@@ -42,6 +44,8 @@ int ilog2(int64_t x) {
   while ((int64_t(1) << r) < x) ++r;
   return r;
 }
+// 16-byte aligned rows of at least n bf16 elements, row stride a multiple of 8 elements
+bool rows_ok(const void* p, int64_t stride, int64_t n) { return aligned(p, 16) && stride % 8 == 0 && stride >= n; }
 
 // Fixed cost of one decode piece, in 64-token blocks of KV traffic: loading the
 // 64 heads' queries (73.7 KB) and writing/merging the partial output.
@@ -53,7 +57,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 7; }
+int mla_abi_version(void) { return 8; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -87,23 +91,32 @@ int mla_store_rows(void* cache, int64_t cache_rows, int64_t cache_row_stride_byt
                     "mla_store_rows launch");
 }
 
-int mla_gather_rows(void* out, int64_t out_row_stride_bytes, const void* cache, int64_t cache_rows,
-                    int64_t cache_row_stride_bytes, const int64_t* indices, int64_t num_rows, int64_t row_bytes,
-                    void* stream) {
-  const char* who = "mla_gather_rows";
-  if (num_rows < 0) return fail(MLA_ERR_INVALID_ARG, "%s: num_rows < 0", who);
-  if (num_rows == 0) return ok();
-  if (out == nullptr || cache == nullptr || indices == nullptr) return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
-  if (row_bytes <= 0 || row_bytes % 16 != 0)
-    return fail(MLA_ERR_UNSUPPORTED, "%s: row_bytes %lld is not a positive multiple of 16", who, (long long)row_bytes);
-  if (out_row_stride_bytes < row_bytes || out_row_stride_bytes % 16 != 0 || cache_row_stride_bytes < row_bytes ||
-      cache_row_stride_bytes % 16 != 0)
-    return fail(MLA_ERR_INVALID_ARG, "%s: strides must be multiples of 16 and >= row_bytes", who);
-  if (!aligned(out, 16) || !aligned(cache, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: 16-byte alignment", who);
-  if (cache_rows <= 0) return fail(MLA_ERR_INVALID_ARG, "%s: cache_rows must be positive", who);
-  return hip_status(mla::launch_gather_rows(out, out_row_stride_bytes, cache, cache_rows, cache_row_stride_bytes, indices,
-                                            num_rows, row_bytes, (hipStream_t)stream),
-                    "mla_gather_rows launch");
+int mla_prefill_gather_bf16(const void* kv_pool, int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
+                            const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens_k,
+                            const int32_t* seg_first, int32_t batch, int32_t max_seg_pages, void* c_out,
+                            int64_t c_row_stride, void* rope_out, int64_t rope_row_stride, int64_t out_rows,
+                            int32_t* seg_page_table, int64_t seg_pt_stride, void* stream) {
+  const char* who = "mla_prefill_gather_bf16";
+  if (batch < 0 || max_seg_pages < 0 || out_rows < 0)
+    return fail(MLA_ERR_INVALID_ARG, "%s: batch %d, max_seg_pages %d, out_rows %lld", who, batch, max_seg_pages,
+                (long long)out_rows);
+  if (batch == 0 || max_seg_pages == 0) return ok();
+  if (kv_pool == nullptr || page_table == nullptr || seq_lens_k == nullptr || seg_first == nullptr ||
+      c_out == nullptr || rope_out == nullptr || seg_page_table == nullptr)
+    return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!is_pow2(page_size)) return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d must be a power of two", who, page_size);
+  if (num_pages < 1 || pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages / pt_stride < 1", who);
+  if (!rows_ok(kv_pool, kv_row_stride, mla::kKvDim) || !rows_ok(c_out, c_row_stride, MLA_V_DIM) ||
+      !rows_ok(rope_out, rope_row_stride, mla::kKvDim - MLA_V_DIM))
+    return fail(MLA_ERR_INVALID_ARG, "%s: rows must be 16-byte aligned with strides multiples of 8 holding the row", who);
+  if (seg_pt_stride < max_seg_pages)
+    return fail(MLA_ERR_INVALID_ARG, "%s: seg_pt_stride %lld < max_seg_pages %d", who, (long long)seg_pt_stride,
+                max_seg_pages);
+  return hip_status(mla::launch_prefill_gather(kv_pool, kv_row_stride, num_pages, ilog2(page_size), page_table,
+                                               pt_stride, seq_lens_k, seg_first, batch, max_seg_pages, c_out,
+                                               c_row_stride, rope_out, rope_row_stride, out_rows, seg_page_table,
+                                               seg_pt_stride, (hipStream_t)stream),
+                    who);
 }
 
 int mla_page_table_from_tokens(const int32_t* token_table, int32_t token_table_rows, int32_t token_table_cols,
@@ -464,30 +477,41 @@ int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slot
   return ok();
 }
 
-int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_pool, int64_t k_row_stride,
-                     const void* v_pool, int64_t v_row_stride, int32_t num_pages, int32_t page_size,
-                     const int32_t* page_table, int64_t pt_stride, const int32_t* cu_seqlens_q,
-                     const int32_t* seq_lens_k, int32_t batch, int32_t total_q, int32_t heads, float scale, void* out,
-                     int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t, void* stream) {
-  const char* who = "mla_prefill_bf16";
+// Shared checks and launch of the prefill entry points; K/V rows as in mla::PrefillParams.
+static int prefill_launch(const char* who, const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_nope,
+                          int64_t k_row_stride, int64_t k_head_stride, const void* k_rope, int64_t k_rope_head_stride,
+                          const void* v, int64_t v_row_stride, int64_t v_head_stride, int32_t num_pages,
+                          int32_t page_size, const int32_t* page_table, int64_t pt_stride, const int32_t* cu_seqlens_q,
+                          const int32_t* seq_lens_k, int32_t batch, int32_t total_q, int32_t heads, float scale,
+                          void* out, int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t,
+                          void* stream) {
   if (batch < 0 || total_q < 0 || heads < 1)
     return fail(MLA_ERR_INVALID_ARG, "%s: batch %d, total_q %d, heads %d", who, batch, total_q, heads);
   if (batch == 0 || total_q == 0) return ok();
-  if (q == nullptr || k_pool == nullptr || v_pool == nullptr || page_table == nullptr || cu_seqlens_q == nullptr ||
-      seq_lens_k == nullptr || out == nullptr)
+  if (q == nullptr || k_nope == nullptr || k_rope == nullptr || v == nullptr || page_table == nullptr ||
+      cu_seqlens_q == nullptr || seq_lens_k == nullptr || out == nullptr)
     return fail(MLA_ERR_INVALID_ARG, "%s: null pointer", who);
   if (!is_pow2(page_size) || page_size < 64)
     return fail(MLA_ERR_UNSUPPORTED, "%s: page_size %d must be a power of two >= 64", who, page_size);
   if (num_pages < 1 || pt_stride < 1) return fail(MLA_ERR_INVALID_ARG, "%s: num_pages / pt_stride < 1", who);
-  if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(out, 8))
+  if (!aligned(q, 16) || !aligned(k_nope, 16) || !aligned(k_rope, 16) || !aligned(v, 16) || !aligned(out, 8))
     return fail(MLA_ERR_INVALID_ARG, "%s: q/k/v must be 16-byte and out 8-byte aligned", who);
   if (q_stride_t % 8 || q_stride_h % 8 || q_stride_h < mla::kPrefillQkDim)
     return fail(MLA_ERR_INVALID_ARG, "%s: q strides (%lld, %lld) must be multiples of 8 with head stride >= 192", who,
                 (long long)q_stride_t, (long long)q_stride_h);
-  if (k_row_stride % 8 || k_row_stride < (int64_t)heads * mla::kPrefillQkDim || v_row_stride % 8 ||
-      v_row_stride < (int64_t)heads * mla::kPrefillVDim)
-    return fail(MLA_ERR_INVALID_ARG, "%s: k/v row strides (%lld, %lld) must be multiples of 8 and hold %d heads", who,
+  if (k_row_stride % 8 || k_head_stride % 8 || k_rope_head_stride % 8 || v_row_stride % 8 || v_head_stride % 8 ||
+      k_head_stride < 0 || k_rope_head_stride < 0 || v_head_stride < 0)
+    return fail(MLA_ERR_INVALID_ARG, "%s: k/v strides must be non-negative multiples of 8", who);
+  if (k_row_stride < (heads - 1) * k_head_stride + 128 || v_row_stride < (heads - 1) * v_head_stride + mla::kPrefillVDim)
+    return fail(MLA_ERR_INVALID_ARG, "%s: k/v row strides (%lld, %lld) must hold %d heads", who,
                 (long long)k_row_stride, (long long)v_row_stride, heads);
+  // the rope dims are addressed relative to the same head's nope dims, within 2 GiB after them
+  const int64_t d0 = static_cast<const char*>(k_rope) - static_cast<const char*>(k_nope);
+  const int64_t dh = 2 * (k_rope_head_stride - k_head_stride);
+  const int64_t d_first = d0, d_last = d0 + (int64_t)(heads - 1) * dh;
+  if (std::min(d_first, d_last) < 256 || std::max(d_first, d_last) >= ((int64_t)1 << 31) - 64 * k_row_stride)
+    return fail(MLA_ERR_UNSUPPORTED,
+                "%s: the rope dims of every head must lie between 256 bytes and 2 GiB after its nope dims", who);
   if ((int64_t)page_size * k_row_stride * 2 > (int64_t)UINT32_MAX ||
       (int64_t)page_size * v_row_stride * 2 > (int64_t)UINT32_MAX)
     return fail(MLA_ERR_UNSUPPORTED, "%s: one page of k/v rows exceeds 4 GiB", who);
@@ -501,10 +525,14 @@ int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   p.q = static_cast<const __bf16*>(q);
   p.q_stride_t = q_stride_t;
   p.q_stride_h = q_stride_h;
-  p.k = static_cast<const __bf16*>(k_pool);
+  p.k = static_cast<const __bf16*>(k_nope);
   p.k_row_stride = k_row_stride;
-  p.v = static_cast<const __bf16*>(v_pool);
+  p.k_head_stride = k_head_stride;
+  p.k_rope_delta0 = d0;
+  p.k_rope_delta_h = dh;
+  p.v = static_cast<const __bf16*>(v);
   p.v_row_stride = v_row_stride;
+  p.v_head_stride = v_head_stride;
   p.num_pages = num_pages;
   p.log2_ps = ilog2(page_size);
   p.page_table = page_table;
@@ -519,10 +547,37 @@ int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   p.out_stride_h = out_stride_h;
   p.lse = lse;
   p.lse_stride_t = lse_stride_t;
-  return hip_status(mla::launch_prefill(p, total_q, (hipStream_t)stream), "mla_prefill_bf16 launch");
+  return hip_status(mla::launch_prefill(p, total_q, (hipStream_t)stream), who);
 }
 
-static bool rows_ok(const void* p, int64_t stride, int64_t n) { return aligned(p, 16) && stride % 8 == 0 && stride >= n; }
+int mla_prefill_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_pool, int64_t k_row_stride,
+                     const void* v_pool, int64_t v_row_stride, int32_t num_pages, int32_t page_size,
+                     const int32_t* page_table, int64_t pt_stride, const int32_t* cu_seqlens_q,
+                     const int32_t* seq_lens_k, int32_t batch, int32_t total_q, int32_t heads, float scale, void* out,
+                     int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t, void* stream) {
+  const char* who = "mla_prefill_bf16";
+  if (heads >= 1 && (k_row_stride < (int64_t)heads * mla::kPrefillQkDim || v_row_stride < (int64_t)heads * mla::kPrefillVDim))
+    return fail(MLA_ERR_INVALID_ARG, "%s: k/v row strides (%lld, %lld) must hold %d heads", who,
+                (long long)k_row_stride, (long long)v_row_stride, heads);
+  const void* k_rope = k_pool == nullptr ? nullptr : static_cast<const __bf16*>(k_pool) + 128;
+  return prefill_launch(who, q, q_stride_t, q_stride_h, k_pool, k_row_stride, mla::kPrefillQkDim, k_rope,
+                        mla::kPrefillQkDim, v_pool, v_row_stride, mla::kPrefillVDim, num_pages, page_size, page_table,
+                        pt_stride, cu_seqlens_q, seq_lens_k, batch, total_q, heads, scale, out, out_stride_t,
+                        out_stride_h, lse, lse_stride_t, stream);
+}
+
+int mla_prefill_strided_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_nope,
+                             int64_t k_row_stride, int64_t k_head_stride, const void* k_rope, int64_t k_rope_head_stride,
+                             const void* v, int64_t v_row_stride, int64_t v_head_stride, int32_t num_pages,
+                             int32_t page_size, const int32_t* page_table, int64_t pt_stride,
+                             const int32_t* cu_seqlens_q, const int32_t* seq_lens_k, int32_t batch, int32_t total_q,
+                             int32_t heads, float scale, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                             float* lse, int64_t lse_stride_t, void* stream) {
+  return prefill_launch("mla_prefill_strided_bf16", q, q_stride_t, q_stride_h, k_nope, k_row_stride, k_head_stride,
+                        k_rope, k_rope_head_stride, v, v_row_stride, v_head_stride, num_pages, page_size, page_table,
+                        pt_stride, cu_seqlens_q, seq_lens_k, batch, total_q, heads, scale, out, out_stride_t,
+                        out_stride_h, lse, lse_stride_t, stream);
+}
 
 int mla_rmsnorm_bf16(const void* x, int64_t x_row_stride, const void* weight, int32_t rows, int32_t n, float eps,
                      void* out, int64_t out_row_stride, void* stream) {

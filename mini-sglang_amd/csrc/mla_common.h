@@ -78,10 +78,13 @@ constexpr int kPrefillRows = 256;  // query rows per CTA (64 per wave)
 struct PrefillParams {
   const __bf16* q;  // [T, H, 192]
   int64_t q_stride_t, q_stride_h;
-  const __bf16* k;  // [pages * ps, H, 192]: token row stride k_row_stride, head stride 192
-  int64_t k_row_stride;
-  const __bf16* v;  // [pages * ps, H, 128]
-  int64_t v_row_stride;
+  // K row of (token row r, head h): 128 nope dims at k + r * k_row_stride + h * k_head_stride, then
+  // 64 rope dims k_rope_delta0 + h * k_rope_delta_h bytes after the nope dims' start
+  const __bf16* k;
+  int64_t k_row_stride, k_head_stride;
+  int64_t k_rope_delta0, k_rope_delta_h;
+  const __bf16* v;  // V row: 128 dims at v + r * v_row_stride + h * v_head_stride
+  int64_t v_row_stride, v_head_stride;
   int32_t num_pages;
   int32_t log2_ps;
   const int32_t* page_table;
@@ -106,15 +109,17 @@ int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64
 int api_error(int code, const char* fmt, ...);
 
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream);
+hipError_t launch_prefill_gather(const void* kv, int64_t kv_row_stride, int32_t num_pages, int32_t log2_ps,
+                                 const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens_k,
+                                 const int32_t* seg_first, int32_t batch, int32_t max_seg_pages, void* c_out,
+                                 int64_t c_row_stride, void* rope_out, int64_t rope_row_stride, int64_t out_rows,
+                                 int32_t* seg_pt, int64_t seg_pt_stride, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_decode_ws(const DecodeParams& p, hipStream_t stream);      // heads 64, pages >= 32
 hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
 hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
                              const void* indices, int index_bits, int64_t rows, int64_t row_bytes,
                              hipStream_t stream);
-hipError_t launch_gather_rows(void* out, int64_t out_stride, const void* cache, int64_t cache_rows,
-                              int64_t cache_stride, const int64_t* indices, int64_t rows, int64_t row_bytes,
-                              hipStream_t stream);
 hipError_t launch_page_table(const int32_t* tt, int32_t tt_rows, int64_t tt_stride, const int32_t* table_idx,
                              int32_t batch, int32_t cols, int32_t page_size, int32_t* out,
                              int64_t out_stride, hipStream_t stream);

@@ -1,6 +1,9 @@
 // Chunked MLA prefill (non-absorbed form), causal and bottom-right aligned over
 // a paged prefix: query i of a request with prefix P attends keys j <= P + i.
-// Per head: q [192] (128 nope + 64 rope), K [192], V [128].
+// Per head: q [192] (128 nope + 64 rope), K [192], V [128]. A K row is read from two places: its
+// 128 nope dims and, a per-head byte offset after them, its 64 rope dims (the per-head page layout
+// [.., H, 192] has them adjacent; the latent-decompression scratch keeps one rope copy per token,
+// shared by all heads, after the heads' [k_nope | v] blocks).
 //
 // One CTA per (request, 256 query rows, head); 4 waves x 64 query rows (two
 // 32-row sub-blocks), one wave per SIMD.
@@ -186,9 +189,16 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   const int c32 = lane & 31;
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
-  const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * kPKRowBytes;
-  const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * kPVRowBytes;
+  // a K row is 128 nope dims at kbase (+ token row) and 64 rope dims rope_delta bytes after them
+  // (the host checks 0 <= rope_delta < 2^31 for every head)
+  const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
+  const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * p.v_head_stride * 2;
+  const uint32_t rope_delta = (uint32_t)(p.k_rope_delta0 + (int64_t)h * p.k_rope_delta_h);
   const int krow_bytes = (int)(p.k_row_stride * 2), vrow_bytes = (int)(p.v_row_stride * 2);
+  // source byte offset of logical K chunk c (16 bytes; 0..15 nope, 16..23 rope) of a row
+  auto kchunk_src = [&](int c) __attribute__((always_inline)) {
+    return c < 16 ? (uint32_t)(c * 16) : rope_delta + (uint32_t)((c - 16) * 16);
+  };
   // bytes of one page of K / V rows (< 4 GiB, checked by the host)
   const uint32_t kpage_bytes = (uint32_t)krow_bytes << p.log2_ps, vpage_bytes = (uint32_t)vrow_bytes << p.log2_ps;
   // first source row of the stage that starts at token t0, on page pid
@@ -228,7 +238,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
   for (int k = 0; k < kPKDma; ++k) {
     const int s = (wave + k * kPWaves) * 64 + lane, t = s / 24;
-    koff[k] = (uint32_t)(t * krow_bytes + kswz(s - 24 * t, t) * 16);
+    koff[k] = (uint32_t)(t * krow_bytes) + kchunk_src(kswz(s - 24 * t, t));
   }
 #pragma unroll
   for (int k = 0; k < kPVDma; ++k) {
@@ -263,7 +273,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int k = 0; k < kPKDma; ++k) {
       const int s = (wave + k * kPWaves) * 64 + ln, t = s / 24;
-      const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes + kswz(s - 24 * t, t) * 16);
+      const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes) + kchunk_src(kswz(s - 24 * t, t));
       dma16_saddr(ksrc, o, st + (wave + k * kPWaves) * 1024);
     }
 #pragma unroll

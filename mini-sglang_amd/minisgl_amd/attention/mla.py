@@ -10,11 +10,13 @@ with the attention math in libmla_amd.so:
   gather kernel) and -- for decode -- a split-KV plan computed on the host by
   the library's planner (the role FlashInfer's plan() plays in fi.py:123-166).
   Host arrays go to the device with pinned non-blocking copies (fa.py:76-90).
-* ``forward`` stores the new rows into the pool (fa.py:53) and runs, for a
-  decode batch, the absorbed decode kernel: ``q [B, H, 576]`` -> ``o [B, H,
-  512]`` (latent space; the caller applies W_UV); for a prefill batch, the
-  chunked prefill kernel over the per-head K/V pages: ``q [T, H, 192]`` -> ``o
-  [T, H, 128]``.
+* ``forward`` stores the new latent rows into the pool (fa.py:53) and runs,
+  for a decode batch, the absorbed decode kernel: ``q [B, H, 576]`` -> ``o
+  [B, H, 512]`` (latent space; the caller applies W_UV); for a prefill batch,
+  the chunked prefill over the keys decompressed from the latent pool: a HIP
+  gather of every key's latent row into 64-token scratch pages, one GEMM
+  ``[k_nope | v] = c W_kvb^T`` (the layer registers its ``W_kvb``), then the
+  prefill kernel: ``q [T, H, 192]`` -> ``o [T, H, 128]``. Any page size.
 * the capture hooks point the metadata at static buffers sized for the
   largest captured batch (fa.py:107-136); replay copies the live metadata in.
 """
@@ -37,8 +39,38 @@ from .utils import BaseCaptureData
 _CPU_I32 = {"device": "cpu", "dtype": torch.int32, "pin_memory": True}
 
 
-# the prefill kernel reads keys in 64-token tiles that must lie inside one page
+# the prefill kernel reads keys in 64-token tiles that must lie inside one page: the decompression
+# scratch is laid out in pages of this many rows
 PREFILL_PAGE = 64
+# decompression scratch rows (keys of one prefill pass) unless the backend is given another bound;
+# at 64 heads a row is (64 * 256 + 64 + 512) * 2 = 33,920 bytes, so 65,536 rows are 2.2 GB
+DEFAULT_PREFILL_SCRATCH_ROWS = 65536
+
+
+def prefill_scratch_bytes(num_heads: int, rows: int) -> int:
+    """Device bytes of a decompression scratch of ``rows`` keys: per key one row
+    ``[head 0: k_nope 128 | v 128, ..., rope 64]`` plus its 512 latent dims (the GEMM input)."""
+    return rows * (num_heads * 256 + 64 + 512) * 2
+
+
+def prefill_passes(seqlens_k: List[int], cap_rows: int) -> List[Tuple[int, int, List[int]]]:
+    """Split a prefill batch into passes of consecutive whole requests whose keys fit ``cap_rows``
+    scratch rows (each request rounded up to 64-row pages); a request longer than the scratch is a
+    pass of its own (the scratch then grows to hold it). Returns ``(r0, r1, seg_first)`` per pass:
+    requests ``r0 .. r1 - 1``, request ``r0 + i`` starting at scratch page ``seg_first[i]``."""
+    passes: List[Tuple[int, int, List[int]]] = []
+    r0, first = 0, []
+    used = 0
+    for r, L in enumerate(seqlens_k):
+        pages = -(-L // PREFILL_PAGE)
+        if first and (used + pages) * PREFILL_PAGE > cap_rows:
+            passes.append((r0, r, first))
+            r0, first, used = r, [], 0
+        first.append(used)
+        used += pages
+    if first:
+        passes.append((r0, len(seqlens_k), first))
+    return passes
 
 
 @dataclass
@@ -57,16 +89,21 @@ class MLAMetadata(BaseAttnMetadata):
     is_decode: bool
     plan: torch.Tensor | None = None  # decode split-KV plan (device)
     num_slots: int = 0
-    seqlens_k: List[int] | None = None  # host copy of cache_seqlens (prefill batches)
     num_ctas: int = 0  # grid of the decode launch (the plan's CTA count)
     workspace: Tuple[torch.Tensor, torch.Tensor] | None = None  # split-KV partials (decode)
+    # prefill: passes (r0, r1, scratch rows, max pages per request, offset of the pass's seg_first in
+    # prefill_seg_first, query rows)
+    prefill_plan: List[Tuple[int, int, int, int, int, int]] | None = None
+    prefill_seg_first: torch.Tensor | None = None  # int32 (device): each pass's first scratch pages
+    prefill_seg_pt: torch.Tensor | None = None  # int32 [bs, max pages] scratch page table (device)
 
     def get_last_indices(self, bs: int) -> torch.Tensor:
         return self.cu_seqlens_q[1 : 1 + bs] - 1
 
 
 class MLAAttnBackend(BaseAttnBackend):
-    def __init__(self, config: MLAConfig, num_ctas: int | None = None):
+    def __init__(self, config: MLAConfig, num_ctas: int | None = None,
+                 prefill_scratch_rows: int = DEFAULT_PREFILL_SCRATCH_ROWS):
         ctx = get_global_ctx()
         assert isinstance(ctx.kv_cache, MLAKVCache), "the MLA backend needs an MLAKVCache pool"
         self.config = config
@@ -90,6 +127,13 @@ class MLAAttnBackend(BaseAttnBackend):
         self.ws_eager: Tuple[torch.Tensor, torch.Tensor] | None = None
         self.ws_graph: Tuple[torch.Tensor, torch.Tensor] | None = None
         self.last_lse: torch.Tensor | None = None  # natural-log LSE of the last forward
+        # prefill decompression: the layers' W_kvb [H * (128 + 128), 512] and a scratch of
+        # prefill_scratch_rows keys (allocated at the first prefill, grown for a longer request)
+        assert prefill_scratch_rows >= PREFILL_PAGE
+        self.prefill_scratch_rows = prefill_scratch_rows
+        self.kv_b: dict = {}
+        self.scratch_rows: torch.Tensor | None = None  # [rows, H * 256 + 64]: [k_nope | v] per head, rope
+        self.scratch_c: torch.Tensor | None = None  # [rows, 512] latent dims (the GEMM input)
 
     # ------------------------------------------------------------------ workspace
     def _new_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -105,7 +149,17 @@ class MLAAttnBackend(BaseAttnBackend):
         return self.ws_eager
 
     # ------------------------------------------------------------------ forward
+    def register_kv_b(self, layer_id: int, kv_b: torch.Tensor) -> None:
+        """The decompression weight of layer ``layer_id``: ``kv_b [H * (128 + 128), 512]`` bf16, head
+        h's rows ``256h .. 256h + 127`` give its k_nope, the next 128 its v (DeepSeek-V3's
+        ``kv_b_proj`` layout). Prefill batches of that layer decompress the latent keys with it."""
+        H = self.num_heads
+        assert kv_b.shape == (H * 256, self.config.kv_lora_rank) and kv_b.dtype == torch.bfloat16
+        self.kv_b[layer_id] = kv_b
+
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_id: int, batch: Batch) -> torch.Tensor:
+        """``k [T, 576]``: the new tokens' latent rows (``v`` unused: the values are their first 512
+        dims), stored into the pool; then decode (``q [B, H, 576]``) or prefill (``q [T, H, 192]``)."""
         metadata = batch.attn_metadata
         assert isinstance(metadata, MLAMetadata)
         self.kvcache.store_kv(k, v, batch.out_loc, layer_id)
@@ -122,52 +176,44 @@ class MLAAttnBackend(BaseAttnBackend):
         self.last_lse = lse
         return out
 
-    def _forward_prefill(self, q: torch.Tensor, layer_id: int, metadata: MLAMetadata) -> torch.Tensor:
-        """Chunked prefill, non-absorbed: ``q [T, H, 192]`` over the per-head K/V pages -> ``[T, H, 128]``.
+    def _prefill_scratch(self, rows: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self.scratch_rows is None or self.scratch_rows.shape[0] < rows:
+            n = max(rows, min(self.prefill_scratch_rows, 4 * rows))
+            n = -(-n // PREFILL_PAGE) * PREFILL_PAGE
+            self.scratch_rows = self.scratch_c = None
+            H, dev = self.num_heads, self.device
+            self.scratch_rows = torch.empty((n, H * 256 + 64), dtype=torch.bfloat16, device=dev)
+            self.scratch_c = torch.empty((n, self.config.kv_lora_rank), dtype=torch.bfloat16, device=dev)
+        return self.scratch_rows, self.scratch_c
 
-        The new tokens' K/V were stored above; every request attends its prefix and itself causally
-        (bottom-right aligned, ``attention/fa.py:155``)."""
+    def _forward_prefill(self, q: torch.Tensor, layer_id: int, md: MLAMetadata) -> torch.Tensor:
+        """Chunked prefill from the latent pool: ``q [T, H, 192]`` -> ``[T, H, 128]``.
+
+        Per pass of whole requests: the latent rows of every key (prefix and chunk, already in the
+        pool) are gathered into 64-token scratch pages (HIP, bit-exact), decompressed per head by one
+        GEMM ``[k_nope | v] = c W_kvb^T`` (hipBLASLt) into the same scratch rows, whose tail keeps the
+        key's shared rope dims; the prefill kernel then attends every request's prefix and itself
+        causally (bottom-right aligned, ``attention/fa.py:155``) over those pages."""
+        kv_b = self.kv_b.get(layer_id)
+        if kv_b is None:
+            raise lib.MLAKernelError(f"layer {layer_id}: no W_kvb registered (register_kv_b) for prefill")
         T, H, _ = q.shape
         out = torch.empty((T, H, self.config.v_head_dim), dtype=q.dtype, device=q.device)
         lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
-        k_pages, v_pages = self.kvcache.prefill_k_cache(layer_id), self.kvcache.prefill_v_cache(layer_id)
-        page_table = metadata.page_table
-        if self.page_size < PREFILL_PAGE:
-            k_pages, v_pages, page_table = self._prefill_pages_of(k_pages, v_pages, metadata)
-        lib.mla_prefill(
-            q, k_pages, v_pages, page_table, metadata.cu_seqlens_q, metadata.cache_seqlens, self.scale, out, lse,
-        )
+        pool = self.kvcache.latent_cache(layer_id)
+        need = max(p[2] for p in md.prefill_plan)
+        srows, sc = self._prefill_scratch(need)
+        width = H * 256
+        for r0, r1, rows, max_pages, off, q_rows in md.prefill_plan:
+            n = r1 - r0
+            seg_pt = md.prefill_seg_pt[r0:r1]
+            lib.prefill_gather(pool, md.page_table[r0:r1], md.cache_seqlens[r0:r1], md.prefill_seg_first[off : off + n],
+                               max_pages, sc[:rows], srows[:rows, width:], seg_pt)
+            torch.mm(sc[:rows], kv_b.t(), out=srows[:rows, :width])
+            lib.mla_prefill_decompressed(q, srows[:rows], seg_pt, md.cu_seqlens_q[r0 : r1 + 1],
+                                         md.cache_seqlens[r0:r1], q_rows, self.scale, out, lse)
         self.last_lse = lse
         return out
-
-    def _prefill_pages_of(self, k_pool: torch.Tensor, v_pool: torch.Tensor, md: MLAMetadata):
-        """Pools with pages smaller than the prefill kernel's 64-token key tile (the reference's
-        default page size is 1, python/minisgl/engine/config.py:25): every request's K/V rows are
-        gathered on the device into consecutive 64-token pages of a scratch pool, with a page table
-        over it, and the prefill kernel runs on those."""
-        ps, H = self.page_size, k_pool.shape[-2]
-        lens = md.seqlens_k
-        pages = [-(-L // PREFILL_PAGE) for L in lens]
-        first = [0]
-        for n in pages:
-            first.append(first[-1] + n)
-        dev = k_pool.device
-        k_tmp = torch.empty((max(first[-1], 1), PREFILL_PAGE, H, k_pool.shape[-1]), dtype=k_pool.dtype, device=dev)
-        v_tmp = torch.empty((max(first[-1], 1), PREFILL_PAGE, H, v_pool.shape[-1]), dtype=v_pool.dtype, device=dev)
-        kf, vf = k_pool.view(-1, H * k_pool.shape[-1]), v_pool.view(-1, H * v_pool.shape[-1])
-        ktf, vtf = k_tmp.view(-1, H * k_pool.shape[-1]), v_tmp.view(-1, H * v_pool.shape[-1])
-        for b, L in enumerate(lens):
-            if L == 0:
-                continue
-            t = torch.arange(L, device=dev)
-            src = md.page_table[b, t // ps].long() * ps + t % ps  # the request's pool rows
-            dst0 = first[b] * PREFILL_PAGE
-            lib.gather_rows(ktf[dst0 : dst0 + L], kf, src)
-            lib.gather_rows(vtf[dst0 : dst0 + L], vf, src)
-        width = max(max(pages), 1)
-        pt = torch.tensor([[first[b] + min(j, max(n - 1, 0)) for j in range(width)] for b, n in enumerate(pages)],
-                          dtype=torch.int32).to(dev, non_blocking=True)
-        return k_tmp, v_tmp, pt
 
     def _plan(self, seqlens_k: List[int], grid: int | None = None):
         """Split plan on the smallest grid of ``num_ctas * 2^k`` CTAs that holds the batch (one CTA per
@@ -239,6 +285,19 @@ class MLAAttnBackend(BaseAttnBackend):
                 workspace = self._eager_workspace(slots)
             assert slots <= workspace[0].shape[0]
             plan_dev = torch.from_numpy(plan_np).pin_memory().to(device, non_blocking=True)
+        prefill_plan = seg_first_dev = seg_pt = None
+        if not is_decode:
+            prefill_plan, firsts = [], []
+            max_pages_all = 0
+            for r0, r1, first in prefill_passes(seqlens_k, self.prefill_scratch_rows):
+                pages = [-(-L // PREFILL_PAGE) for L in seqlens_k[r0:r1]]
+                rows = (first[-1] + pages[-1]) * PREFILL_PAGE
+                max_pages = max(max(pages), 1)
+                max_pages_all = max(max_pages_all, max_pages)
+                prefill_plan.append((r0, r1, max(rows, PREFILL_PAGE), max_pages, len(firsts), sum(seqlens_q[r0:r1])))
+                firsts += first
+            seg_first_dev = torch.tensor(firsts, **_CPU_I32).to(device, non_blocking=True)
+            seg_pt = torch.empty((padded_size, max_pages_all), dtype=torch.int32, device=device)
         batch.attn_metadata = MLAMetadata(
             cu_seqlens_k=cu_seqlens_k,
             cu_seqlens_q=cu_seqlens_q,
@@ -249,9 +308,11 @@ class MLAAttnBackend(BaseAttnBackend):
             is_decode=is_decode,
             plan=plan_dev,
             num_slots=slots,
-            seqlens_k=None if is_decode else seqlens_k,
             num_ctas=ctas if is_decode else 0,
             workspace=workspace,
+            prefill_plan=prefill_plan,
+            prefill_seg_first=seg_first_dev,
+            prefill_seg_pt=seg_pt,
         )
 
     # ------------------------------------------------------------------ graph capture

@@ -76,17 +76,11 @@ class LayerBench:
         self.ctx = Context(page_size=PAGE)
         set_global_ctx(self.ctx)
         self.ctx.page_table = tt.to(dev)
-        pool = create_kvcache_pool(self.cfg.attn, num_pages, PAGE, torch.bfloat16, dev,
-                                   with_prefill_pages=(phase == "prefill"))
+        pool = create_kvcache_pool(self.cfg.attn, num_pages, PAGE, torch.bfloat16, dev)
         self.ctx.kv_cache = pool
         gd = torch.Generator(device=dev).manual_seed(seed + 2)
-        caches = [pool.latent_cache(i) for i in range(2)]
-        if phase == "prefill":
-            caches += [pool.prefill_k_cache(i) for i in range(2)] + [pool.prefill_v_cache(i) for i in range(2)]
-        for c in caches:  # fill page by page: the per-head pages are GBs
-            step = max(1, (1 << 26) // c[0].numel())
-            for p0 in range(0, c.shape[0], step):
-                c[p0 : p0 + step] = torch.randn(c[p0 : p0 + step].shape, generator=gd, device=dev).to(torch.bfloat16)
+        for c in [pool.latent_cache(i) for i in range(2)]:
+            c.copy_(torch.randn(c.shape, generator=gd, device=dev).to(torch.bfloat16))
         self.backend = create_attention_backend("mla", self.cfg.attn)
         self.ctx.attn_backend = self.backend
         self.layers = [MLAAttentionLayer(i, self.cfg, MLAWeights.random(self.cfg, gen, dev)) for i in range(2)]

@@ -28,7 +28,10 @@ SIGNATURES = {
     "mla_abi_version": (ctypes.c_int, []),
     "mla_device_cu_count": (ctypes.c_int, [ctypes.c_int, _c_i32p]),
     "mla_store_rows": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp]),
-    "mla_gather_rows": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
+    "mla_prefill_gather_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
     "mla_page_table_from_tokens": (
         ctypes.c_int,
         [_vp, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _vp],
@@ -57,6 +60,11 @@ SIGNATURES = {
         [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32, _i32, ctypes.c_float,
          _vp, _i64, _i64, _vp, _i64, _vp],
     ),
+    "mla_prefill_strided_bf16": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _i32,
+         _i32, ctypes.c_float, _vp, _i64, _i64, _vp, _i64, _vp],
+    ),
     "mla_rmsnorm_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i32, _i32, ctypes.c_float, _vp, _i64, _vp]),
     "mla_latent_rows_bf16": (
         ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _i32, _vp, _i64, _vp]
@@ -70,7 +78,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
@@ -299,6 +307,75 @@ def mla_prefill(q, k_pool, v_pool, page_table, cu_seqlens_q, seq_lens_k, scale: 
     )
 
 
+def mla_prefill_strided(q, k_nope, k_row_stride: int, k_head_stride: int, k_rope, k_rope_head_stride: int, v,
+                        v_row_stride: int, v_head_stride: int, num_pages: int, page_size: int, page_table,
+                        cu_seqlens_q, seq_lens_k, total_q: int, scale: float, out, lse=None, stream=None) -> None:
+    """``mla_prefill`` with K and V rows anywhere (``mla_prefill_strided_bf16``): ``k_nope``,
+    ``k_rope`` and ``v`` are bf16 tensors whose first elements are those of token row 0 / head 0;
+    strides in elements; token row r = page * page_size + offset. ``total_q`` bounds the launch
+    (at least the query rows of this batch)."""
+    import torch
+
+    T, H, D = q.shape
+    assert D == 192 and q.dtype == torch.bfloat16 and q.stride(-1) == 1
+    for t in (k_nope, k_rope, v):
+        assert t.dtype == torch.bfloat16 and t.is_cuda
+    assert page_table.dtype == torch.int32 and cu_seqlens_q.dtype == torch.int32 and seq_lens_k.dtype == torch.int32
+    assert out.shape == (T, H, 128) and out.dtype == torch.bfloat16 and out.stride(-1) == 1
+    B = seq_lens_k.shape[0]
+    assert cu_seqlens_q.shape[0] == B + 1
+    if lse is not None:
+        assert lse.dtype == torch.float32 and lse.shape == (T, H) and lse.stride(-1) == 1
+    check(
+        load_library().mla_prefill_strided_bf16(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(k_nope), k_row_stride, k_head_stride, _ptr(k_rope),
+            k_rope_head_stride, _ptr(v), v_row_stride, v_head_stride, num_pages, page_size, _ptr(page_table),
+            page_table.stride(0), _ptr(cu_seqlens_q), _ptr(seq_lens_k), B, total_q, H, float(scale), _ptr(out),
+            out.stride(0), out.stride(1), _ptr(lse), 0 if lse is None else lse.stride(0), _stream(stream),
+        ),
+        "mla_prefill_strided_bf16",
+    )
+
+
+def mla_prefill_decompressed(q, rows, page_table, cu_seqlens_q, seq_lens_k, total_q: int, scale: float, out,
+                             lse=None, stream=None) -> None:
+    """Prefill over decompressed scratch rows ``rows [n, H * 256 + 64]`` (per key: head h's k_nope
+    at ``256h``, its v at ``256h + 128``, the shared rope dims at ``256H``), in 64-row pages under
+    ``page_table`` (``prefill_gather``'s scratch page table)."""
+    H = q.shape[1]
+    n, width = rows.shape
+    assert width == 256 * H + 64 and rows.stride(1) == 1 and n % 64 == 0
+    stride = rows.stride(0)
+    mla_prefill_strided(q, rows, stride, 256, rows[:, 256 * H :], 0, rows[:, 128:], stride, 256, n // 64, 64,
+                        page_table, cu_seqlens_q, seq_lens_k, total_q, scale, out, lse, stream)
+
+
+def prefill_gather(kv_pool, page_table, seq_lens_k, seg_first, max_seg_pages: int, c_out, rope_out, seg_page_table,
+                   stream=None) -> None:
+    """``mla_prefill_gather_bf16``: key j of request b (pool ``kv_pool [pages, ps, 576]`` through
+    ``page_table``) to scratch row ``64 seg_first[b] + j`` of ``c_out [rows, 512]`` (latent dims)
+    and ``rope_out [rows, 64]`` (rope dims); ``seg_page_table[b, i] = seg_first[b] + i``."""
+    import torch
+
+    assert kv_pool.dim() == 3 and kv_pool.shape[-1] == 576 and kv_pool.dtype == torch.bfloat16
+    assert kv_pool.stride(-1) == 1 and kv_pool.stride(0) == kv_pool.shape[1] * kv_pool.stride(1)
+    assert c_out.shape[1] == 512 and rope_out.shape[1] == 64 and c_out.shape[0] == rope_out.shape[0]
+    assert c_out.stride(1) == 1 and rope_out.stride(1) == 1
+    for t in (page_table, seq_lens_k, seg_first, seg_page_table):
+        assert t.dtype == torch.int32
+    B = seq_lens_k.shape[0]
+    assert seg_first.shape[0] >= B and seg_page_table.shape[0] >= B and seg_page_table.shape[1] >= max_seg_pages
+    check(
+        load_library().mla_prefill_gather_bf16(
+            _ptr(kv_pool), kv_pool.stride(1), kv_pool.shape[0], kv_pool.shape[1], _ptr(page_table),
+            page_table.stride(0), _ptr(seq_lens_k), _ptr(seg_first), B, max_seg_pages, _ptr(c_out), c_out.stride(0),
+            _ptr(rope_out), rope_out.stride(0), c_out.shape[0], _ptr(seg_page_table), seg_page_table.stride(0),
+            _stream(stream),
+        ),
+        "mla_prefill_gather_bf16",
+    )
+
+
 def rmsnorm(x, weight, eps: float, out=None, stream=None):
     """``x [rows, n]`` bf16 -> ``x / sqrt(mean(x^2) + eps) * weight`` (``out`` may be ``x``)."""
     import torch
@@ -388,23 +465,3 @@ def qkv_a_rows(qkv, q_rank: int, q_norm_weight, kv_norm_weight, positions, cos_s
         "mla_qkv_a_rows_bf16",
     )
     return out
-
-
-def gather_rows(out, cache, indices, stream=None) -> None:
-    """``out[i] = cache[indices[i]]`` over the leading dims (int64 indices; the inverse of store_rows)."""
-    import torch
-
-    assert out.is_cuda and cache.is_cuda and indices.is_cuda and out.dtype == cache.dtype
-    assert indices.dim() == 1 and indices.dtype == torch.int64 and indices.is_contiguous()
-    n = indices.shape[0]
-    o2, c2 = out.view(out.shape[0], -1), cache.view(cache.shape[0], -1)
-    row_bytes = c2.shape[1] * c2.element_size()
-    assert o2.shape[1] * o2.element_size() == row_bytes and o2.shape[0] >= n
-    assert o2.stride(-1) == 1 and c2.stride(-1) == 1
-    check(
-        load_library().mla_gather_rows(
-            _ptr(o2), o2.stride(0) * o2.element_size(), _ptr(c2), c2.shape[0], c2.stride(0) * c2.element_size(),
-            _ptr(indices), n, row_bytes, _stream(stream),
-        ),
-        "mla_gather_rows",
-    )

@@ -17,7 +17,6 @@ def create_kvcache_pool(
     page_size: int,
     dtype: torch.dtype,
     device: torch.device,
-    with_prefill_pages: bool = False,
 ) -> BaseKVCachePool:
     return MLAKVCache(
         num_layers=model_config.num_layers,
@@ -27,9 +26,6 @@ def create_kvcache_pool(
         device=device,
         kv_lora_rank=model_config.kv_lora_rank,
         qk_rope_head_dim=model_config.qk_rope_head_dim,
-        prefill_heads=model_config.num_heads if with_prefill_pages else 0,
-        qk_head_dim=model_config.qk_head_dim,
-        v_head_dim=model_config.v_head_dim,
     )
 
 

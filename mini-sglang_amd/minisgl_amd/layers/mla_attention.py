@@ -14,13 +14,14 @@ KV pool):
 * decode (absorbed): ``q_lat = q_nope W_UK`` -> ``[T, H, 512]``, the backend attends
   ``[q_lat | q_pe]`` over the latent rows ``[c | k_pe]`` and returns ``o_lat [T, H, 512]``,
   then ``o = o_lat W_UV^T`` -> ``[T, H, 128]``;
-* prefill (decompressed): ``k = [k_nope | k_pe]`` ``[T, H, 192]`` and ``v [T, H, 128]``, the
-  backend attends ``q`` causally over the per-head pages;
+* prefill (decompressed): the backend stores the chunk's latent rows, decompresses every key of
+  each request (prefix and chunk) from the latent pool with this layer's ``W_kvb`` into
+  ``k = [k_nope | k_pe]`` and ``v`` per head, and attends ``q`` causally over them;
 * ``out = W_o . o``.
 
-Every new token's latent row is stored (decode reads it); when the pool also holds per-head
-pages, every new token's decompressed K/V is stored there too, so a later prefill chunk (or a
-new request reusing this prefix) finds its whole prefix decompressed.
+The pool holds only latent rows (1152 bytes per token and layer); both phases read them, so a
+prefix cached by one request (or by earlier chunks of the same request) serves decode and prefill
+alike.
 
 RoPE: the cos/sin cache of python/minisgl/layers/rotary.py:22-31 (``[max_position, d]``, the
 ``d/2`` cosines then the ``d/2`` sines) with its YaRN frequency blend (rotary.py:92-111);
@@ -197,24 +198,12 @@ class MLAAttentionLayer:
         self.w_qkv_a = torch.cat((weights.q_a, weights.kv_a), dim=0).contiguous()
         self.w_uk = weights.w_uk(a).contiguous()  # [H, 128, 512]
         self.w_uv_t = weights.w_uv(a).transpose(1, 2).contiguous()  # [H, 512, 128]
-        self.w_uk_flat = self.w_uk.reshape(-1, a.kv_lora_rank)  # [H*128, 512]
-        self.w_uv_flat = weights.w_uv(a).reshape(-1, a.kv_lora_rank).contiguous()  # [H*128, 512]
-
-    def _decompress(self, latent: torch.Tensor):
-        """Per-head ``k [T, H, 192]`` and ``v [T, H, 128]`` of latent rows ``[T, 576]``."""
-        a = self.cfg.attn
-        T = latent.shape[0]
-        c = latent[:, : a.kv_lora_rank]
-        k_nope = (c @ self.w_uk_flat.t()).view(T, a.num_heads, a.qk_nope_head_dim)
-        v = (c @ self.w_uv_flat.t()).view(T, a.num_heads, a.v_head_dim)
-        k_pe = latent[:, None, a.kv_lora_rank :].expand(T, a.num_heads, a.qk_rope_head_dim)
-        return torch.cat((k_nope, k_pe), dim=-1), v
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """``x [T, hidden]`` (the tokens of ``ctx.batch``, in batch order) -> ``[T, hidden]``."""
         a = self.cfg.attn
         ctx = get_global_ctx()
-        batch, backend, pool = ctx.batch, ctx.attn_backend, ctx.kv_cache
+        batch, backend = ctx.batch, ctx.attn_backend
         T, H = x.shape[0], a.num_heads
         ops, eps, inter = self.ops, self.cfg.rms_eps, self.cfg.rope_interleaved
         pos = batch.positions.to(torch.int32)  # no copy when the scheduler already gives int32
@@ -231,17 +220,13 @@ class MLAAttentionLayer:
             ops.q_rope(q, pos, self.cos_sin, inter, q_abs[..., a.kv_lora_rank :], q_nope_h.transpose(0, 1))
             # the bmm writes each head's q_nope W_UK straight into the absorbed query's first 512 dims
             torch.bmm(q_nope_h, self.w_uk, out=q_abs[..., : a.kv_lora_rank].transpose(0, 1))
-            if pool.has_prefill_pages:  # keep the per-head pages whole for a later prefill over this prefix
-                k, v = self._decompress(latent)
-                pool.store_kv(k, v, batch.out_loc, self.layer_id)
             o_lat = backend.forward(q_abs, latent, None, self.layer_id, batch)  # stores the latent rows
             # o[t, h] = o_lat[t, h] W_UV[h]^T, read and written through head-major views (no copies)
             o = torch.empty((T, H, a.v_head_dim), dtype=x.dtype, device=x.device)
             torch.bmm(o_lat.transpose(0, 1), self.w_uv_t, out=o.transpose(0, 1))
         else:
-            pool.store_kv(latent, None, batch.out_loc, self.layer_id)  # for the decode steps to come
             ops.q_rope(q, pos, self.cos_sin, inter, q[..., a.qk_nope_head_dim :])  # in place
-            k, v = self._decompress(latent)
-            # the backend stores k / v in the per-head pages, then attends over prefix + chunk
-            o = backend.forward(q, k, v, self.layer_id, batch)
+            # the backend stores the latent rows, then decompresses prefix + chunk with W_kvb
+            backend.register_kv_b(self.layer_id, self.w.kv_b)
+            o = backend.forward(q, latent, None, self.layer_id, batch)
         return o.reshape(T, H * a.v_head_dim) @ self.w.o.t()

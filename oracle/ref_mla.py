@@ -33,13 +33,20 @@ What it restates, and from where:
   bottom-right alignment: query ``i`` of a request with ``L`` total and ``E``
   new tokens sits at absolute position ``L - E + i`` and sees keys ``j <= L -
   E + i`` (``attention/fa.py:84-90,155``; lengths from ``core.py:44-50``).
+* ``decompress_pool`` -- per-head K/V of latent rows, the decompression the MLA
+  layer does before a chunked prefill (the caller role of
+  ``layers/attention.py:47-57``, MLA having no code in the reference): with
+  ``W_kvb [H * 256, 512]`` (head ``h``'s rows ``256h .. 256h + 127`` give its
+  k_nope, the next 128 its v), ``K[t, h] = [W_kvb[256h : 256h+128] c_t | k_pe_t]``
+  and ``V[t, h] = W_kvb[256h+128 : 256h+256] c_t``.
 
 Empty inputs: a request with zero keys yields ``o = 0`` and ``lse = -inf``.
 
 Pins (tests/test_oracle.py): float64 pure-Python loops on tiny inputs, the
 closed forms (one key, equal scores, dominant key, score shift), torch's
 ``scaled_dot_product_attention`` on CPU, split/merge equivalence, the
-absorbed-vs-decompressed MLA identity and the reference's own bit-exact store
+absorbed-vs-decompressed MLA identity (through ``decompress_pool``), scalar loops
+for ``decompress_pool`` and the reference's own bit-exact store
 and page-table invariants (``tests/kernel/test_store.py:33-34``,
 ``tests/core/test_cache_allocate.py:147-169``).
 """
@@ -85,6 +92,22 @@ def token_rows(page_table_row: torch.Tensor, length: int, page_size: int) -> tor
     t = torch.arange(length, dtype=torch.int64)
     pages = page_table_row.long()[t // page_size]
     return pages * page_size + t % page_size
+
+
+def decompress_pool(latent_pool: torch.Tensor, kv_b: torch.Tensor, num_heads: int, out_dtype=None):
+    """Per-head pages ``K [pages, ps, H, 192]``, ``V [pages, ps, H, 128]`` of a latent pool
+    ``[pages, ps, 576]`` with ``kv_b [H * 256, 512]`` (float32 math, float64 for float64 inputs);
+    ``out_dtype`` rounds K and V to it (the GPU path writes bf16 decompressed rows)."""
+    dt = torch.float64 if latent_pool.dtype == torch.float64 else torch.float32
+    pages, ps, _ = latent_pool.shape
+    rows = latent_pool.reshape(-1, KV_DIM).to(dt)
+    w = kv_b.to(dt).view(num_heads, 2, 128, LATENT_DIM)  # [head][k_nope | v][dim][latent]
+    kv = torch.einsum("tl,hjdl->thjd", rows[:, :LATENT_DIM], w)  # [rows, H, 2, 128]
+    k = torch.cat([kv[:, :, 0], rows[:, None, LATENT_DIM:].expand(-1, num_heads, -1)], dim=-1)
+    v = kv[:, :, 1]
+    if out_dtype is not None:
+        k, v = k.to(out_dtype), v.to(out_dtype)
+    return k.reshape(pages, ps, num_heads, PREFILL_QK_DIM), v.reshape(pages, ps, num_heads, PREFILL_V_DIM)
 
 
 def gather_rows(pool_flat: torch.Tensor, page_table_row: torch.Tensor, length: int, page_size: int):

@@ -149,39 +149,44 @@ def test_backend_decode_graph_replay(page_size, graph_max_len):
             r.complete_one()
 
 
-@pytest.mark.parametrize("page_size", [64, 32, 16, 1])
-def test_backend_prefill_with_prefix(page_size):
-    """A prefill batch through the backend: the new per-head K/V rows are stored
-    at out_loc, then every request attends its cached prefix and itself causally.
-    Pages smaller than 64 tokens (the reference's default page size is 1) go through
-    the backend's gather into 64-token scratch pages."""
-    print(f"[backend prefill] page_size={page_size}", flush=True)
+def _prefill_setup(page_size, cached, extends, H=16, seed=5, scratch_rows=None):
+    """Context, latent pool (random rows on 2 layers), token table and backend for a prefill batch."""
     reset_global_ctx()
-    H = 16
     ctx = Context(page_size=page_size)
     set_global_ctx(ctx)
-    gen = torch.Generator().manual_seed(5)
+    gen = torch.Generator().manual_seed(seed)
     cfg = MLAConfig(num_heads=H, num_layers=2)
-    cached, extends = [0, 130, 64, 700], [300, 1, 77, 129]
     lens = [c + e for c, e in zip(cached, extends)]
     need = [-(-L // page_size) for L in lens]
     num_pages = sum(need) + 3
-    pool = create_kvcache_pool(cfg, num_pages, page_size, torch.bfloat16, DEV, with_prefill_pages=True)
+    pool = create_kvcache_pool(cfg, num_pages, page_size, torch.bfloat16, DEV)
     ctx.kv_cache = pool
-    tt = torch.zeros((len(lens) + 1, 1024), dtype=torch.int32)
+    width = -(-max(n * page_size for n in need) // 32) * 32
+    tt = torch.zeros((len(lens) + 1, width), dtype=torch.int32)
     starts = torch.randperm(num_pages, generator=gen)[: sum(need)] * page_size
     off = 0
     for r, n in enumerate(need):
         tt[r, : n * page_size] = (starts[off : off + n].unsqueeze(1) + torch.arange(page_size)).flatten().to(torch.int32)
         off += n
     ctx.page_table = tt.to(DEV)
-    layer = 1
-    kc, vc = pool.prefill_k_cache(layer), pool.prefill_v_cache(layer)
-    kc.copy_(torch.randn(kc.shape, generator=gen).to(torch.bfloat16).to(DEV))
-    vc.copy_(torch.randn(vc.shape, generator=gen).to(torch.bfloat16).to(DEV))
-    backend = create_attention_backend("mla", cfg)
-    ctx.attn_backend = backend
+    for layer in range(2):
+        c = pool.latent_cache(layer)
+        c.copy_(torch.randn(c.shape, generator=gen).to(torch.bfloat16).to(DEV))
+    if scratch_rows is None:
+        backend = create_attention_backend("mla", cfg)
+    else:
+        from minisgl_amd.attention.mla import MLAAttnBackend
 
+        backend = MLAAttnBackend(cfg, prefill_scratch_rows=scratch_rows)
+    ctx.attn_backend = backend
+    kv_b = (torch.randn((H * 256, 512), generator=gen) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
+    return ctx, pool, backend, tt, lens, kv_b, gen
+
+
+def _run_prefill(ctx, pool, backend, tt, cached, extends, kv_b, gen, layer=1, H=16):
+    """One prefill batch through backend.forward (latent rows of the chunk stored, prefix + chunk
+    decompressed with kv_b); returns (o, lse, batch, q) and checks the stored rows bit for bit."""
+    backend.register_kv_b(layer, kv_b)
     reqs = [Req(table_idx=i, cached_len=c, device_len=c + e) for i, (c, e) in enumerate(zip(cached, extends))]
     batch = Batch(reqs=reqs, phase="prefill")
     batch.padded_reqs = reqs
@@ -190,24 +195,62 @@ def test_backend_prefill_with_prefix(page_size):
     backend.prepare_metadata(batch)
     T = sum(extends)
     q = torch.randn((T, H, 192), generator=gen).to(torch.bfloat16).to(DEV)
-    k_new = torch.randn((T, H, 192), generator=gen).to(torch.bfloat16).to(DEV)
-    v_new = torch.randn((T, H, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    k_new = torch.randn((T, 576), generator=gen).to(torch.bfloat16).to(DEV)
     with ctx.forward_batch(batch):
-        o = backend.forward(q, k_new, v_new, layer, batch)
+        o = backend.forward(q, k_new, None, layer, batch)
     torch.cuda.synchronize()
-    loc = batch.out_loc.long()
-    assert torch.equal(kc.reshape(-1, H, 192)[loc].view(torch.int16), k_new.view(torch.int16))
-    assert torch.equal(vc.reshape(-1, H, 128)[loc].view(torch.int16), v_new.view(torch.int16))
+    stored = pool.latent_cache(layer).reshape(-1, 576)[batch.out_loc.long()]
+    assert torch.equal(stored.view(torch.int16), k_new.view(torch.int16))
+    return o, backend.last_lse, batch, q
 
-    idx = torch.arange(len(reqs), dtype=torch.int32)
+
+def _prefill_expected(pool, tt, cached, extends, kv_b, q, layer, page_size, H):
+    """Oracle: the latent pool decompressed per head (bf16 rows, as the GPU's GEMM writes them), then
+    chunked prefill over it."""
+    lens = [c + e for c, e in zip(cached, extends)]
+    K, V = R.decompress_pool(pool.latent_cache(layer).cpu(), kv_b.cpu(), H, out_dtype=torch.bfloat16)
+    idx = torch.arange(len(lens), dtype=torch.int32)
     pt = R.page_table_from_tokens(tt, idx, max(lens), page_size)
-    cu = torch.tensor([0] + extends, dtype=torch.int32).cumsum(0).to(torch.int32)
-    o_ref, lse_ref = R.mla_prefill(q.cpu(), kc.cpu(), vc.cpu(), pt, cu, torch.tensor(lens, dtype=torch.int32))
+    cu = torch.tensor([0] + list(extends), dtype=torch.int32).cumsum(0).to(torch.int32)
+    return R.mla_prefill(q.cpu(), K, V, pt, cu, torch.tensor(lens, dtype=torch.int32)), cu
+
+
+@pytest.mark.parametrize("page_size", [128, 64, 32, 16, 1])
+def test_backend_prefill_from_latent_pool(page_size):
+    """A prefill batch through the backend over a latent-only pool: the chunk's latent rows are
+    stored at out_loc (bit-exact), every key of each request (cached prefix and chunk) is gathered
+    into 64-token scratch pages and decompressed per head with the layer's W_kvb, and every request
+    attends its prefix and itself causally. Any pool page size (the reference's default is 1)."""
+    print(f"[backend prefill] page_size={page_size}", flush=True)
+    H = 16
+    cached, extends = [0, 130, 64, 700], [300, 1, 77, 129]
+    ctx, pool, backend, tt, lens, kv_b, gen = _prefill_setup(page_size, cached, extends, H)
+    o, lse, batch, q = _run_prefill(ctx, pool, backend, tt, cached, extends, kv_b, gen, H=H)
+    (o_ref, lse_ref), cu = _prefill_expected(pool, tt, cached, extends, kv_b, q, 1, page_size, H)
+    T = sum(extends)
     assert o.shape == (T, H, 128)
     torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
-    torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
+    torch.testing.assert_close(lse.cpu(), lse_ref, **LSE_TOL)
     md = batch.attn_metadata
-    assert torch.equal(md.get_last_indices(len(reqs)).cpu(), cu[1:] - 1)
+    assert len(md.prefill_plan) == 1
+    assert torch.equal(md.get_last_indices(len(lens)).cpu(), cu[1:] - 1)
+    reset_global_ctx()
+
+
+def test_backend_prefill_in_passes():
+    """A decompression scratch of 512 rows: the batch runs as several passes of whole requests, one
+    request (1300 keys) longer than the scratch, which then grows to hold it."""
+    H = 16
+    cached, extends = [100, 300, 1200, 0, 40, 64], [28, 100, 100, 200, 1, 63]
+    ctx, pool, backend, tt, lens, kv_b, gen = _prefill_setup(64, cached, extends, H, seed=8, scratch_rows=512)
+    o, lse, batch, q = _run_prefill(ctx, pool, backend, tt, cached, extends, kv_b, gen, H=H)
+    plan = batch.attn_metadata.prefill_plan
+    print(f"[prefill passes] {[(p[0], p[1], p[2]) for p in plan]}", flush=True)
+    assert len(plan) >= 3 and any(p[2] > 512 for p in plan)
+    (o_ref, lse_ref), _ = _prefill_expected(pool, tt, cached, extends, kv_b, q, 1, 64, H)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(lse.cpu(), lse_ref, **LSE_TOL)
+    reset_global_ctx()
 
 
 def test_backend_eager_batch_after_capture():

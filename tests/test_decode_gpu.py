@@ -269,21 +269,48 @@ def test_decode_long_context_split_kv():
     torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
 
 
-@pytest.mark.parametrize("row_elems", [576, 16 * 192])
-def test_gather_rows_bit_exact(row_elems):
-    """mla_gather_rows: out[i] = cache[idx[i]] bit for bit (the inverse of store_rows), repeated and
-    out-of-range indices included (an out-of-range row is left untouched)."""
-    g = torch.Generator().manual_seed(row_elems)
-    cache = torch.randn((300, row_elems), generator=g).to(torch.bfloat16).to(DEV)
-    idx = torch.randint(0, 300, (257,), generator=g)
-    idx[5] = idx[6]
-    idx[9] = 300  # out of range
-    out = torch.full((257, row_elems), 3.0, dtype=torch.bfloat16, device=DEV)
-    lib.gather_rows(out, cache, idx.to(DEV))
+@pytest.mark.parametrize("ps", [1, 16, 64, 128])
+def test_prefill_gather_bit_exact(ps):
+    """mla_prefill_gather_bf16: every key's latent row (through the page table, any page size) lands
+    bit for bit in its 64-row scratch page (latent dims and rope dims in their own row-strided
+    buffers), rows past a request's keys stay untouched, and the scratch page table is
+    seg_first[b] + i. Includes an empty request and page ids outside the pool (clamped)."""
+    g = torch.Generator().manual_seed(ps)
+    lens = [1, 64, 65, 0, 300, 129]
+    pages = [-(-L // ps) for L in lens]
+    num_pages = sum(pages) + 2
+    pool = torch.randn((num_pages, ps, 576), generator=g).to(torch.bfloat16)
+    width = max(max(pages), 1) + 1
+    pt = torch.randint(0, num_pages, (len(lens), width), generator=g).to(torch.int32)
+    pt[4, 0] = num_pages + 5  # out of range: clamped to the last page
+    seg_pages = [-(-L // 64) for L in lens]
+    seg_first = [0]
+    for n in seg_pages[:-1]:
+        seg_first.append(seg_first[-1] + n + 1)  # a gap page between requests
+    rows = (seg_first[-1] + seg_pages[-1] + 1) * 64
+    c = torch.full((rows, 520), 7.0, dtype=torch.bfloat16, device=DEV)  # row stride 520 > 512
+    tail = torch.full((rows, 80), 7.0, dtype=torch.bfloat16, device=DEV)
+    seg_pt = torch.full((len(lens), max(seg_pages) + 1), -1, dtype=torch.int32, device=DEV)
+    lib.prefill_gather(pool.to(DEV), pt.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                       torch.tensor(seg_first, dtype=torch.int32, device=DEV), max(seg_pages), c[:, :512],
+                       tail[:, 8:72], seg_pt)
     torch.cuda.synchronize()
-    ok = idx < 300
-    assert torch.equal(out[ok.to(DEV)].view(torch.int16), cache[idx[ok].to(DEV)].view(torch.int16))
-    assert torch.all(out[9] == 3.0)
+    c, tail, seg_pt = c.cpu(), tail.cpu(), seg_pt.cpu()
+    flat = pool.reshape(-1, 576)
+    written = torch.zeros(rows, dtype=torch.bool)
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        ptb = pt[b].clamp(0, num_pages - 1)
+        src = flat[R.token_rows(ptb, L, ps)]
+        dst = seg_first[b] * 64 + torch.arange(L)
+        assert torch.equal(c[dst, :512].view(torch.int16), src[:, :512].view(torch.int16))
+        assert torch.equal(tail[dst, 8:72].view(torch.int16), src[:, 512:].view(torch.int16))
+        written[dst] = True
+        assert seg_pt[b, : seg_pages[b]].tolist() == [seg_first[b] + i for i in range(seg_pages[b])]
+    assert torch.all(c[~written] == 7.0) and torch.all(c[:, 512:] == 7.0)
+    assert torch.all(tail[~written] == 7.0) and torch.all(tail[:, :8] == 7.0) and torch.all(tail[:, 72:] == 7.0)
+    assert seg_pt[3].tolist() == [-1] * seg_pt.shape[1]  # the empty request writes no page
 
 
 def _one_hot_targets(L, ps):

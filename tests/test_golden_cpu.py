@@ -87,3 +87,35 @@ def test_layer_op_argument_errors_are_reported():
     rc = so.mla_qkv_a_rows_bf16(p, 2112, 1530, p, p, p, p, 16, 4, 1e-6, 1, p, 576, None)
     assert rc != 0 and b"q_rank" in so.mla_last_error()
     assert so.mla_rmsnorm_bf16(None, 0, None, 0, 8, 1e-6, None, 0, None) == 0  # no rows: nothing to do
+
+
+def test_prefill_entry_argument_errors_are_reported():
+    """The prefill entry points' C-ABI checks (layouts the kernel cannot address) fire before any
+    device work."""
+    from minisgl_amd.kernel import lib
+
+    so = lib.load_library()
+    buf = ctypes.create_string_buffer(1 << 20)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256  # aligned host address, never dereferenced
+    H, row = 16, 16 * 256 + 64
+
+    def strided(k_rope_off, k_head=256, k_rope_head=0, row_stride=row, page_size=64):
+        return so.mla_prefill_strided_bf16(p, H * 192, 192, p, row_stride, k_head, p + k_rope_off, k_rope_head,
+                                          p + 256, row_stride, 256, 4, page_size, p, 4, p, p, 2, 10, H, 0.1, p,
+                                          H * 128, 128, None, 0, None)
+
+    # rope dims before a head's nope dims (head 15's rope would sit 256 B before its nope start)
+    rc = strided(2 * 256 * (H - 1) - 256)
+    assert rc != 0 and b"rope dims" in so.mla_last_error()
+    rc = strided(2 * 256 * H, row_stride=15 * 256)  # rows too short for 16 heads
+    assert rc != 0 and b"hold 16 heads" in so.mla_last_error()
+    rc = strided(2 * 256 * H, page_size=32)
+    assert rc != 0 and b"page_size" in so.mla_last_error()
+    rc = so.mla_prefill_gather_bf16(p, 576, 4, 48, p, 4, p, p, 2, 3, p, 512, p, 64, 256, p, 3, None)
+    assert rc != 0 and b"power of two" in so.mla_last_error()
+    rc = so.mla_prefill_gather_bf16(p, 576, 4, 16, p, 4, p, p, 2, 3, p, 512, p, 64, 256, p, 2, None)
+    assert rc != 0 and b"seg_pt_stride" in so.mla_last_error()
+    rc = so.mla_prefill_gather_bf16(p, 576, 4, 16, p, 4, p, p, 2, 3, p, 500, p, 64, 256, p, 3, None)
+    assert rc != 0 and b"strides" in so.mla_last_error()
+    assert so.mla_prefill_gather_bf16(None, 0, 0, 1, None, 0, None, None, 0, 0, None, 0, None, 0, 0, None, 0,
+                                      None) == 0  # no requests: nothing to do

@@ -44,7 +44,8 @@ def test_mixed_config5_full_size_through_backend():
     start with the same page ids, as a radix-cache hit gives them, python/minisgl/kvcache/
     radix_cache.py:132-175), 64 heads, page 64. mini-sglang runs a batch as either prefill or decode
     (python/minisgl/core.py:71-97), so the two halves are two batches through one backend's
-    prepare_metadata + forward over one pool and one token table; each against the oracle."""
+    prepare_metadata + forward over one latent pool and one token table; each against the oracle
+    (prefill: the oracle's decompression of the latent pool, then its chunked prefill)."""
     from minisgl_amd.attention import create_attention_backend
     from minisgl_amd.config import MLAConfig
     from minisgl_amd.core import Batch, Context, Req, reset_global_ctx, set_global_ctx
@@ -59,11 +60,9 @@ def test_mixed_config5_full_size_through_backend():
     set_global_ctx(ctx)
     cfg = MLAConfig(num_heads=H, num_layers=1)
     num_pages = d.kv_pool.shape[0]
-    pool = create_kvcache_pool(cfg, num_pages, ps, torch.bfloat16, DEV, with_prefill_pages=True)
+    pool = create_kvcache_pool(cfg, num_pages, ps, torch.bfloat16, DEV)
     pool.latent_cache(0).copy_(d.kv_pool)
     P = p.k_pool.shape[0]  # the prefill chunks read pages [0, P) only
-    pool.prefill_k_cache(0)[:P].copy_(p.k_pool)
-    pool.prefill_v_cache(0)[:P].copy_(p.v_pool)
     ctx.kv_cache = pool
     nd, npf = len(d.lens), len(p.extends)
     width = -(-max(d.page_table.shape[1], p.page_table.shape[1]) * ps // 32) * 32
@@ -90,21 +89,23 @@ def test_mixed_config5_full_size_through_backend():
     torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
     del o_ref, lse_ref
 
-    # prefill half: each chunk extends its group's 2048-token prefix by 1024 tokens
+    # prefill half: each chunk extends its group's 2048-token prefix by 1024 tokens; the keys (the
+    # shared prefix and the chunk) are decompressed from the latent pool with the layer's W_kvb
+    gen = torch.Generator().manual_seed(3)
+    kv_b = (torch.randn((H * 256, 512), generator=gen) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
+    backend.register_kv_b(0, kv_b)
     reqs = [Req(table_idx=nd + i, cached_len=P0, device_len=P0 + E)
             for i, (P0, E) in enumerate(zip(p.prefixes, p.extends))]
     batch = Batch(reqs=reqs, phase="prefill")
     batch.padded_reqs = reqs
     batch.out_loc = torch.cat([tt[r.table_idx, r.cached_len : r.device_len] for r in reqs])
     backend.prepare_metadata(batch)
-    loc = batch.out_loc.long()
-    k_new = pool.prefill_k_cache(0).view(-1, H, 192)[loc].clone()
-    v_new = pool.prefill_v_cache(0).view(-1, H, 128)[loc].clone()
+    k_new = pool.latent_cache(0).view(-1, 576)[batch.out_loc.long()].clone()
     with ctx.forward_batch(batch):
-        o = backend.forward(p.q, k_new, v_new, 0, batch)
+        o = backend.forward(p.q, k_new, None, 0, batch)
     torch.cuda.synchronize()
-    o_ref, lse_ref = R.mla_prefill(p.q.cpu(), p.k_pool.cpu(), p.v_pool.cpu(), p.page_table.cpu(),
-                                   p.cu_seqlens_q.cpu(), p.seq_lens_k.cpu())
+    K, V = R.decompress_pool(pool.latent_cache(0)[:P].cpu(), kv_b.cpu(), H, out_dtype=torch.bfloat16)
+    o_ref, lse_ref = R.mla_prefill(p.q.cpu(), K, V, p.page_table.cpu(), p.cu_seqlens_q.cpu(), p.seq_lens_k.cpu())
     torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
     torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
     reset_global_ctx()

@@ -196,32 +196,30 @@ def test_rms_norm_closed_form():
 
 
 class _DensePool:
-    """Dense stand-in for the MLA pool: latent rows and per-head pages indexed by token location."""
+    """Dense stand-in for the MLA pool: latent rows indexed by token location."""
 
-    has_prefill_pages = True
-
-    def __init__(self, num_tokens, heads):
+    def __init__(self, num_tokens):
         self.latent = torch.zeros((num_tokens, 576))
-        self.k = torch.zeros((num_tokens, heads, 192))
-        self.v = torch.zeros((num_tokens, heads, 128))
 
     def store_kv(self, k, v, out_loc, layer_id):
-        loc = out_loc.long()
-        if k.dim() == 2:
-            self.latent[loc] = k.float()
-        else:
-            self.k[loc], self.v[loc] = k.float(), v.float()
+        assert k.dim() == 2
+        self.latent[out_loc.long()] = k.float()
 
 
 class _DenseBackend:
-    """Dense stand-in for the MLA backend's contract: store, then decode over latent rows
-    (``q [B, H, 576]`` -> ``[B, H, 512]``) or causal prefill over per-head pages."""
+    """Dense stand-in for the MLA backend's contract: store the latent rows, then decode over them
+    (``q [B, H, 576]`` -> ``[B, H, 512]``) or causal prefill over the keys decompressed from them with
+    the layer's registered ``W_kvb``."""
 
     def __init__(self, pool, tt, scale):
         self.pool, self.tt, self.scale = pool, tt, scale
+        self.kv_b = {}
 
     def prepare_metadata(self, batch):
         batch.attn_metadata = None
+
+    def register_kv_b(self, layer_id, kv_b):
+        self.kv_b[layer_id] = kv_b
 
     def forward(self, q, k, v, layer_id, batch):
         self.pool.store_kv(k, v, batch.out_loc, layer_id)
@@ -230,15 +228,18 @@ class _DenseBackend:
             rows = self.tt[req.table_idx, : req.device_len].long()
             e = req.extend_len
             qi = q[off : off + e].float().transpose(0, 1)  # [H, e, D]
+            H = qi.shape[0]
+            kv = self.pool.latent[rows]
             if batch.is_decode:
-                kv = self.pool.latent[rows]
-                H = qi.shape[0]
                 o, _ = R._attend(qi, kv.expand(H, -1, -1), kv[:, :512].expand(H, -1, -1), self.scale)
             else:
                 L = req.device_len
+                w = self.kv_b[layer_id].float().view(H, 256, 512)
+                k_nope = torch.matmul(kv[None, :, :512], w[:, :128].transpose(1, 2))  # [H, L, 128]
+                vh = torch.matmul(kv[None, :, :512], w[:, 128:].transpose(1, 2))
+                kh = torch.cat((k_nope, kv[None, :, 512:].expand(H, -1, -1)), dim=-1)
                 mask = torch.arange(L)[None, :] <= (L - e + torch.arange(e))[:, None]
-                o, _ = R._attend(qi, self.pool.k[rows].transpose(0, 1), self.pool.v[rows].transpose(0, 1),
-                                 self.scale, mask[None])
+                o, _ = R._attend(qi, kh, vh, self.scale, mask[None])
             outs.append(o.transpose(0, 1))
             off += e
         return torch.cat(outs).to(q.dtype)
@@ -259,7 +260,7 @@ def test_product_layer_on_dense_stand_in(scaling):
     ctx = Context(page_size=16)
     set_global_ctx(ctx)
     ctx.page_table = tt
-    pool = _DensePool(num_pages * 16, H)
+    pool = _DensePool(num_pages * 16)
     backend = _DenseBackend(pool, tt, attn.softmax_scale)
     ctx.kv_cache, ctx.attn_backend = pool, backend
     x_hist = {r: torch.randn((L, 64), generator=gen) for r, L in lens.items()}

@@ -2,7 +2,7 @@
 
 A serving sequence (two chunked-prefill steps, decode steps, a prefill continuing after decode,
 another decode) runs through ``MLAAttentionLayer`` with bf16 weights, the real MLA pool (latent
-rows + per-head prefill pages on shuffled pages) and the HIP kernels; every step's output is
+rows only, on shuffled pages: prefill decompresses every key from them) and the HIP kernels; every step's output is
 compared with ``oracle/ref_mla_layer.py`` (decompressed, float64, rounded to bf16 where the
 layer keeps bf16 tensors). Tolerance: atol = rtol = 2e-2 elementwise (bf16 outputs), and the
 relative Frobenius error of each step below 1e-2.
@@ -48,7 +48,7 @@ def _run_case(H, hidden, q_lora, steps, page_size=64, seed=0):
     ctx = Context(page_size=page_size)
     set_global_ctx(ctx)
     ctx.page_table = tt.to(DEV)
-    ctx.kv_cache = create_kvcache_pool(attn, num_pages, page_size, torch.bfloat16, DEV, with_prefill_pages=True)
+    ctx.kv_cache = create_kvcache_pool(attn, num_pages, page_size, torch.bfloat16, DEV)
     backend = create_attention_backend("mla", attn)
     ctx.attn_backend = backend
     layer = MLAAttentionLayer(0, cfg, weights)
@@ -120,7 +120,7 @@ def test_mla_layer_with_page_allocator():
     ctx.page_table = torch.zeros((4, 512), dtype=torch.int32, device=DEV)
     alloc = PagedTokenTable(num_pages, ps, ctx.page_table)
     alloc.free_slots = alloc.free_slots[torch.randperm(num_pages, generator=gen).to(DEV)]  # a long-running server's order
-    ctx.kv_cache = create_kvcache_pool(attn, num_pages, ps, torch.bfloat16, DEV, with_prefill_pages=True)
+    ctx.kv_cache = create_kvcache_pool(attn, num_pages, ps, torch.bfloat16, DEV)
     backend = create_attention_backend("mla", attn)
     ctx.attn_backend = backend
     layer = MLAAttentionLayer(0, cfg, weights)
@@ -156,7 +156,7 @@ def test_mla_layer_decode_graph_replay():
     ctx = Context(page_size=64)
     set_global_ctx(ctx)
     ctx.page_table = tt.to(DEV)
-    ctx.kv_cache = create_kvcache_pool(attn, num_pages, 64, torch.bfloat16, DEV, with_prefill_pages=True)
+    ctx.kv_cache = create_kvcache_pool(attn, num_pages, 64, torch.bfloat16, DEV)
     backend = create_attention_backend("mla", attn)
     ctx.attn_backend = backend
     layer = MLAAttentionLayer(0, cfg, weights)

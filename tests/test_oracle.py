@@ -292,6 +292,46 @@ def test_absorbed_equals_decompressed():
     assert torch.allclose(lse_a[0], lse_d[0], atol=1e-9)
 
 
+def test_decompress_pool_scalar_loops():
+    """decompress_pool against float64 loops: K[t, h, d] = sum_i kv_b[256h + d, i] c_t[i] (d < 128),
+    K[t, h, 128 + r] = k_pe_t[r], V[t, h, d] = sum_i kv_b[256h + 128 + d, i] c_t[i]."""
+    gen = torch.Generator().manual_seed(23)
+    H, pages, ps = 2, 2, 2
+    pool = torch.randn((pages, ps, R.KV_DIM), generator=gen, dtype=torch.float64)
+    kv_b = torch.randn((H * 256, R.LATENT_DIM), generator=gen, dtype=torch.float64)
+    K, V = R.decompress_pool(pool, kv_b, H)
+    for p in range(pages):
+        for t in range(ps):
+            row = pool[p, t].tolist()
+            for h in (0, H - 1):
+                for d in (0, 77, 127):
+                    kn = sum(float(kv_b[256 * h + d, i]) * row[i] for i in range(R.LATENT_DIM))
+                    vv = sum(float(kv_b[256 * h + 128 + d, i]) * row[i] for i in range(R.LATENT_DIM))
+                    assert abs(float(K[p, t, h, d]) - kn) < 1e-9 and abs(float(V[p, t, h, d]) - vv) < 1e-9
+                for r in (0, 63):
+                    assert float(K[p, t, h, 128 + r]) == row[R.LATENT_DIM + r]
+
+
+def test_decompress_pool_prefill_equals_absorbed_decode():
+    """A one-token extend over decompress_pool's pages equals absorbed decode over the latent pool
+    with q_abs = [q_nope W_UK | q_pe] and o = o_lat W_UV^T: ties the decompression to decode."""
+    gen = torch.Generator().manual_seed(29)
+    H, L, ps = 3, 13, 4
+    pages = -(-L // ps) + 1
+    pool = torch.randn((pages, ps, R.KV_DIM), generator=gen, dtype=torch.float64)
+    kv_b = torch.randn((H * 256, R.LATENT_DIM), generator=gen, dtype=torch.float64) / 16
+    pt = torch.randperm(pages, generator=gen)[: -(-L // ps)].to(torch.int32).unsqueeze(0)
+    q = torch.randn((1, H, R.PREFILL_QK_DIM), generator=gen, dtype=torch.float64)
+    K, V = R.decompress_pool(pool, kv_b, H)
+    o_dec, lse_d = R.mla_prefill(q, K, V, pt, [0, 1], [L], dtype=torch.float64)
+    w = kv_b.view(H, 2, 128, R.LATENT_DIM)
+    q_abs = torch.cat([torch.einsum("hk,hkl->hl", q[0, :, :128], w[:, 0]), q[0, :, 128:]], dim=1).unsqueeze(0)
+    o_lat, lse_a = R.mla_decode(q_abs, pool, pt, [L], dtype=torch.float64)
+    o_abs = torch.einsum("hl,hdl->hd", o_lat[0], w[:, 1])
+    assert torch.allclose(o_abs, o_dec[0], atol=1e-9)
+    assert torch.allclose(lse_a[0], lse_d[0], atol=1e-9)
+
+
 # ----------------------------------------------------------------------------- page table / store pins
 def _loops_page_table(token_table, table_idx, max_len, ps):
     out = []

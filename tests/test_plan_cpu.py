@@ -164,3 +164,21 @@ def test_capture_grid_grows_with_a_huge_pool():
     lens = rng.integers(100_000, 131_073, size=160).tolist()
     plan, slots, grid = be._plan(lens, be.capture_ctas)
     assert grid == 1024 and sum(t1 - t0 for *_, t0, t1 in plan_pieces(plan, grid, lens)) == sum(lens)
+
+
+def test_prefill_passes_hold_whole_requests_within_the_scratch():
+    """Passes are runs of consecutive whole requests whose 64-row pages fit the scratch; a request
+    longer than the scratch is a pass of its own; seg_first counts pages from the pass start."""
+    from minisgl_amd.attention.mla import prefill_passes
+
+    lens = [128, 400, 1300, 200, 41, 127, 1]
+    passes = prefill_passes(lens, 512)
+    assert passes == [(0, 1, [0]), (1, 2, [0]), (2, 3, [0]), (3, 7, [0, 4, 5, 7])]
+    covered = [r for r0, r1, _ in passes for r in range(r0, r1)]
+    assert covered == list(range(len(lens)))
+    for r0, r1, first in passes:
+        pages = [-(-L // 64) for L in lens[r0:r1]]
+        assert first == [sum(pages[:i]) for i in range(len(pages))]
+        assert r1 - r0 == 1 or sum(pages) * 64 <= 512
+    assert prefill_passes(lens, 1 << 20) == [(0, 7, [0, 2, 9, 30, 34, 35, 37])]
+    assert prefill_passes([], 512) == []

@@ -76,6 +76,35 @@ def test_prefill_long_extend_multiple_blocks():
     check_case(case)
 
 
+@pytest.mark.parametrize("heads", [16, 64])
+def test_prefill_decompressed_layout_bit_exact(heads):
+    """The same K/V values laid out as the latent decompression writes them (per key one row
+    [head h: k_nope | v, ..., rope shared by all heads], 64-row pages in another order) give the
+    per-head page layout's result bit for bit: only the addressing differs
+    (mla_prefill_strided_bf16 vs mla_prefill_bf16)."""
+    g = torch.Generator().manual_seed(heads)
+    case = make_prefill_case(heads, 64, extends=[300, 1, 77], prefixes=[130, 700, 0], seed=heads)
+    rope = torch.randn((case.k_pool.shape[0], 64, 64), generator=g).to(torch.bfloat16)
+    case.k_pool[..., 128:] = rope[:, :, None, :]  # one rope row per token, as MLA's k_pe
+    out_a, lse_a = run_prefill(case)
+    P = case.k_pool.shape[0]
+    perm = torch.randperm(P, generator=g)  # scratch page of pool page p: perm[p]
+    rows = torch.zeros((P, 64, heads * 256 + 64), dtype=torch.bfloat16)
+    rows_h = rows[..., : heads * 256].view(P, 64, heads, 256)
+    rows_h[perm, :, :, :128] = case.k_pool[..., :128]
+    rows_h[perm, :, :, 128:] = case.v_pool
+    rows[perm, :, heads * 256 :] = rope
+    pt = perm[case.page_table.long()].to(torch.int32)
+    T = case.q.shape[0]
+    out = torch.full((T, heads, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((T, heads), float("nan"), dtype=torch.float32, device=DEV)
+    lib.mla_prefill_decompressed(case.q.to(DEV), rows.view(P * 64, -1).to(DEV), pt.to(DEV),
+                                 case.cu_seqlens_q.to(DEV), case.seq_lens_k.to(DEV), T, R.DEFAULT_SCALE, out, lse)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), out_a.to(torch.bfloat16).view(torch.int16))
+    assert torch.equal(lse.cpu(), lse_a)
+
+
 def test_prefill_small_pages_rejected():
     case = make_prefill_case(2, 32, extends=[10], prefixes=[5], seed=1)
     with pytest.raises(lib.MLAKernelError, match="page_size"):
