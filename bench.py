@@ -333,7 +333,7 @@ def bench_prefill(args):
     kern_ms = e0.elapsed_time(e1) / steps
     flops = case.flops()
     achieved = flops / (kern_ms * 1e-3) / 1e12
-    return {
+    res = {
         "workload": "MLA chunked prefill, one layer: B=4, H=64, extend 2048, prefix U[0,8192], qk 192, v 128, page 64",
         "prefixes": prefixes,
         "us_per_layer": round(step_ms * 1e3, 1),
@@ -345,6 +345,24 @@ def bench_prefill(args):
                      "traffic": _committed_traffic(PREFILL_TRAFFIC_FILE)},
         "algorithmic_flops": flops,
     }
+    del case
+    torch.cuda.empty_cache()
+    # the same batch through the backend over a latent-only pool: store the chunk, gather every key,
+    # decompress per head (one GEMM), the prefill kernel; at page 64 and at the reference's default 1
+    from minisgl_amd.benchmark.layer import BackendPrefill
+
+    lens = [P + 2048 for P in prefixes]
+    keys = sum(lens)
+    decomp_flops = keys * 2 * 512 * H * 256
+    res["from_latent_pool"] = {"keys_decompressed": keys, "decompress_gflop": round(decomp_flops / 1e9, 1)}
+    for ps in (64, 1):
+        bp = BackendPrefill(lens, [2048] * 4, ps, dev)
+        ms = _time_device(bp, stream, max(2, args.steps // 10), 2)
+        res["from_latent_pool"][f"page_{ps}_us_per_layer"] = round(ms * 1e3, 1)
+        bp.close()
+        del bp
+        torch.cuda.empty_cache()
+    return res
 
 
 class _DecodeCall:

@@ -6,8 +6,9 @@ weights and KV alternate, so that neither a layer's weights (202 MB) nor its KV 
 256 MB Infinity Cache between its steps, as in a 61-layer model.
 
 Decode: B=64, lengths U[1024, 8192] (the headline attention batch: same seed, same lengths),
-one new token per request, latent-only pool. Prefill: B=4 chunks of 2048 tokens on prefixes
-U[0, 8192] (the prefill attention batch), pool with per-head prefill pages.
+one new token per request. Prefill: B=4 chunks of 2048 tokens on prefixes U[0, 8192] (the prefill
+attention batch), every key (prefix and chunk) decompressed from the latent pool by the backend.
+Both phases run over a latent-only pool.
 """
 
 from __future__ import annotations
@@ -42,14 +43,20 @@ def kimi_k2_layer_config(num_layers: int) -> MLALayerConfig:
 
 
 def gemm_flops_per_token(cfg: MLALayerConfig, decode: bool) -> int:
-    """Projection FLOPs of one token: q_a, q_b, kv_a, o, plus the absorption (decode) or the
-    per-head K/V decompression (prefill)."""
+    """Projection FLOPs of one new token: q_a, q_b, kv_a, o, plus the absorption (decode)."""
     a = cfg.attn
     H, r = a.num_heads, a.kv_lora_rank
     f = cfg.hidden_size * cfg.q_lora_rank + cfg.q_lora_rank * H * a.qk_head_dim + cfg.hidden_size * a.kv_dim
     f += H * a.v_head_dim * cfg.hidden_size
-    f += H * (a.qk_nope_head_dim * r + r * a.v_head_dim) if decode else r * H * (a.qk_nope_head_dim + a.v_head_dim)
+    if decode:
+        f += H * (a.qk_nope_head_dim * r + r * a.v_head_dim)
     return 2 * f
+
+
+def decompress_flops_per_key(cfg: MLALayerConfig) -> int:
+    """Prefill: the per-head K/V decompression of one key, [k_nope | v] = c W_kvb^T."""
+    a = cfg.attn
+    return 2 * a.kv_lora_rank * a.num_heads * (a.qk_nope_head_dim + a.v_head_dim)
 
 
 def weight_bytes(w: MLAWeights) -> int:
@@ -128,6 +135,8 @@ def summary(b: LayerBench, ms: float, attn_flops: int, attn_bytes: int) -> Dict[
     """Layer-step figures: time, tokens/s, projection + attention FLOPs and HBM bytes."""
     decode = b.phase == "decode"
     gemm = gemm_flops_per_token(b.cfg, decode) * b.tokens
+    if not decode:  # every key of every request is decompressed once per layer
+        gemm += decompress_flops_per_key(b.cfg) * sum(b.lens)
     w_bytes = weight_bytes(b.layers[0].w)
     act_bytes = b.tokens * HIDDEN * 2 * 2  # x in, out
     flops = gemm + attn_flops
@@ -141,3 +150,57 @@ def summary(b: LayerBench, ms: float, attn_flops: int, attn_bytes: int) -> Dict[
         "hbm_bytes_min_mb": round((w_bytes + attn_bytes + act_bytes) / 1e6, 1),
         "tb_per_s_min_bytes": round((w_bytes + attn_bytes + act_bytes) / (ms * 1e-3) / 1e12, 3),
     }
+
+
+class BackendPrefill:
+    """The attention backend's prefill path alone over a latent-only pool: store the chunk's latent
+    rows, gather every key into scratch pages, decompress with a random ``W_kvb``, prefill kernel.
+    ``__call__`` is one layer's ``backend.forward``; two layers alternate."""
+
+    def __init__(self, lens: Sequence[int], extends: Sequence[int], page_size: int, dev: torch.device,
+                 seed: int = 0):
+        reset_global_ctx()
+        attn = MLAConfig(num_heads=HEADS, num_layers=2)
+        gen = torch.Generator().manual_seed(seed)
+        need = [-(-L // page_size) for L in lens]
+        num_pages = sum(need) + 1
+        width = -(-max(need) * page_size // 32) * 32
+        tt = torch.zeros((len(lens) + 1, width), dtype=torch.int32)
+        perm = torch.randperm(num_pages, generator=gen)
+        off = 0
+        for b, n in enumerate(need):
+            tt[b, : n * page_size] = (perm[off : off + n, None] * page_size + torch.arange(page_size)).flatten().to(
+                torch.int32)
+            off += n
+        self.ctx = Context(page_size=page_size)
+        set_global_ctx(self.ctx)
+        self.ctx.page_table = tt.to(dev)
+        pool = create_kvcache_pool(attn, num_pages, page_size, torch.bfloat16, dev)
+        self.ctx.kv_cache = pool
+        gd = torch.Generator(device=dev).manual_seed(seed + 2)
+        for i in range(2):
+            c = pool.latent_cache(i)
+            c.copy_(torch.randn(c.shape, generator=gd, device=dev).to(torch.bfloat16))
+        self.backend = create_attention_backend("mla", attn)
+        self.ctx.attn_backend = self.backend
+        for i in range(2):
+            self.backend.register_kv_b(i, (torch.randn((HEADS * 256, 512), generator=gd, device=dev) / 512 ** 0.5)
+                                       .to(torch.bfloat16))
+        reqs = [Req(table_idx=b, cached_len=L - E, device_len=L) for b, (L, E) in enumerate(zip(lens, extends))]
+        self.batch = Batch(reqs=reqs, phase="prefill")
+        self.batch.padded_reqs = reqs
+        self.batch.out_loc = torch.cat([tt[r.table_idx, r.cached_len : r.device_len] for r in reqs]).to(dev)
+        self.backend.prepare_metadata(self.batch)
+        T = sum(extends)
+        self.q = torch.randn((T, HEADS, 192), generator=gd, device=dev).to(torch.bfloat16)
+        self.k_new = torch.randn((T, 576), generator=gd, device=dev).to(torch.bfloat16)
+        self.n = 0
+
+    def __call__(self) -> torch.Tensor:
+        with self.ctx.forward_batch(self.batch):
+            o = self.backend.forward(self.q, self.k_new, None, self.n % 2, self.batch)
+        self.n += 1
+        return o
+
+    def close(self) -> None:
+        reset_global_ctx()
