@@ -347,6 +347,8 @@ def bench_prefill(args):
     }
     del case
     torch.cuda.empty_cache()
+    if args.no_extra:
+        return res
     # the same batch through the backend over a latent-only pool: store the chunk, gather every key,
     # decompress per head (one GEMM), the prefill kernel; at page 64 and at the reference's default 1
     from minisgl_amd.benchmark.layer import BackendPrefill
@@ -594,7 +596,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "long", "mixed", "layer", "peaks"])
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill summary of the decode line")
-    ap.add_argument("--no-extra", action="store_true", help="skip the long-context and mixed-batch summaries")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the long-context and mixed-batch summaries and the prefill-from-latent-pool timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured HBM-read and MFMA peaks")
     args = ap.parse_args()
