@@ -300,7 +300,8 @@ int mla_qkv_a_rows_bf16(void *qkv, int64_t qkv_row_stride, int32_t q_rank, const
  * (q_stride_t, q_stride_h)): pe_out[t, h, 0:64] = RoPE of q[t, h, 128:192] at positions[t]
  * (pe_out may be q + 128 with q's strides: in place); if nope_out is not NULL,
  * nope_out[t, h, 0:128] = q[t, h, 0:128] with its own strides (e.g. head-major for the W_UK
- * absorption GEMM). RoPE conventions as mla_latent_rows_bf16. Replaces the query half of
+ * absorption GEMM). RoPE conventions as mla_latent_rows_bf16. q, pe_out and nope_out are
+ * 16-byte aligned with strides multiples of 8 elements. Replaces the query half of
  * RotaryEmbedding.forward (rotary.py:39-51).
  */
 int mla_q_rope_bf16(const void *q, int64_t q_stride_t, int64_t q_stride_h, int32_t tokens, int32_t heads,

@@ -641,8 +641,9 @@ int mla_q_rope_bf16(const void* q, int64_t q_stride_t, int64_t q_stride_h, int32
   if (!aligned(q, 16) || q_stride_t % 8 || q_stride_h % 8 || q_stride_h < 192 || q_stride_t < heads * q_stride_h)
     return fail(MLA_ERR_INVALID_ARG, "%s: q must be 16-byte aligned, strides multiples of 8 holding %d heads of 192",
                 who, heads);
-  if (pe_stride_h < 64 || pe_stride_t < heads * pe_stride_h)
-    return fail(MLA_ERR_INVALID_ARG, "%s: pe_out strides (%lld, %lld) must hold %d heads of 64", who,
+  if (!aligned(pe_out, 16) || pe_stride_t % 8 || pe_stride_h % 8 || pe_stride_h < 64 || pe_stride_t < heads * pe_stride_h)
+    return fail(MLA_ERR_INVALID_ARG,
+                "%s: pe_out must be 16-byte aligned, strides (%lld, %lld) multiples of 8 holding %d heads of 64", who,
                 (long long)pe_stride_t, (long long)pe_stride_h, heads);
   if (nope_out != nullptr && (!aligned(nope_out, 16) || nope_stride_t % 8 || nope_stride_h % 8 ||
                               (nope_stride_t < nope_stride_h ? nope_stride_t : nope_stride_h) < 128))

@@ -160,24 +160,68 @@ __global__ __launch_bounds__(256) void qkv_a_rows_kernel(__bf16* qkv, int64_t qk
 
 // Query (t, h) = q[t, h, 0:192] (128 nope + 64 rope dims): pe_out[t, h, 0:64] = RoPE of the rope
 // dims at positions[t]; if nope_out is given, nope_out[t, h, 0:128] (own strides, e.g. head-major)
-// = the nope dims. pe_out may alias the rope dims of q (in place). One wave per (t, h).
+// = the nope dims. pe_out may alias the rope dims of q (in place: every lane writes only the
+// bytes it read). One wave per (token, 8 heads): lane 8 hl + k rotates pairs 4k .. 4k + 3 of head
+// 8 g + hl, one 16-byte access (interleaved pairs: dims 8k .. 8k + 7) or two 8-byte ones (halves:
+// dims 4k .. 4k + 3 and 32 + 4k .. 32 + 4k + 3); the nope copy is 128 16-byte chunks per wave.
+constexpr int kQRopeHeads = 8;
+
 __global__ __launch_bounds__(256) void q_rope_kernel(const __bf16* q, int64_t qst, int64_t qsh, int tokens,
                                                      int heads, const int32_t* __restrict__ pos,
                                                      const float* __restrict__ cos_sin, int max_pos, int interleaved,
                                                      __bf16* pe, int64_t pst, int64_t psh, __bf16* __restrict__ nope,
                                                      int64_t nst, int64_t nsh) {
   const int lane = threadIdx.x & 63;
+  const int groups = (heads + kQRopeHeads - 1) / kQRopeHeads;
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= (int64_t)tokens * heads) return;
-  const int t = (int)(item / heads), h = (int)(item % heads);
-  const __bf16* qr = q + (int64_t)t * qst + (int64_t)h * qsh;
-  if (nope != nullptr && lane < kNopeDim / 8)
-    *reinterpret_cast<u32x4*>(nope + (int64_t)t * nst + (int64_t)h * nsh + 8 * lane) =
-        *reinterpret_cast<const u32x4*>(qr + 8 * lane);
-  if (lane >= 32) {
-    const int p = min(max(pos[t], 0), max_pos - 1);
-    rope_pair(qr + kNopeDim, pe + (int64_t)t * pst + (int64_t)h * psh, lane - 32, cos_sin + (int64_t)p * kRopeDim,
-              interleaved);
+  if (item >= (int64_t)tokens * groups) return;
+  const int t = (int)(item / groups), h0 = (int)(item % groups) * kQRopeHeads;
+  if (nope != nullptr) {
+    for (int c = lane; c < kQRopeHeads * (kNopeDim / 8); c += 64) {
+      const int h = h0 + c / (kNopeDim / 8), k = c % (kNopeDim / 8);
+      if (h < heads)
+        *reinterpret_cast<u32x4*>(nope + (int64_t)t * nst + (int64_t)h * nsh + 8 * k) =
+            *reinterpret_cast<const u32x4*>(q + (int64_t)t * qst + (int64_t)h * qsh + 8 * k);
+    }
+  }
+  const int h = h0 + (lane >> 3), k = lane & 7;
+  if (h >= heads) return;
+  const int p = min(max(pos[t], 0), max_pos - 1);
+  const float* cs = cos_sin + (int64_t)p * kRopeDim;
+  const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + 4 * k);
+  const f32x4 sv = *reinterpret_cast<const f32x4*>(cs + kRopeDim / 2 + 4 * k);
+  const __bf16* in = q + (int64_t)t * qst + (int64_t)h * qsh + kNopeDim;
+  __bf16* out = pe + (int64_t)t * pst + (int64_t)h * psh;
+  if (interleaved) {
+    float f[8], g[8];
+    unpack8(*reinterpret_cast<const u32x4*>(in + 8 * k), f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g[2 * i] = f[2 * i] * cv[i] - f[2 * i + 1] * sv[i];
+      g[2 * i + 1] = f[2 * i + 1] * cv[i] + f[2 * i] * sv[i];
+    }
+    *reinterpret_cast<u32x4*>(out + 8 * k) = pack8(g);
+  } else {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(in + 4 * k);
+    const u32x2 b = *reinterpret_cast<const u32x2*>(in + kRopeDim / 2 + 4 * k);
+    float xa[4], xb[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      xa[2 * i] = __uint_as_float(a[i] << 16);
+      xa[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+      xb[2 * i] = __uint_as_float(b[i] << 16);
+      xb[2 * i + 1] = __uint_as_float(b[i] & 0xffff0000u);
+    }
+    u32x2 ra, rb;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ra[i] = pack_bf16x2(xa[2 * i] * cv[2 * i] - xb[2 * i] * sv[2 * i],
+                          xa[2 * i + 1] * cv[2 * i + 1] - xb[2 * i + 1] * sv[2 * i + 1]);
+      rb[i] = pack_bf16x2(xb[2 * i] * cv[2 * i] + xa[2 * i] * sv[2 * i],
+                          xb[2 * i + 1] * cv[2 * i + 1] + xa[2 * i + 1] * sv[2 * i + 1]);
+    }
+    *reinterpret_cast<u32x2*>(out + 4 * k) = ra;
+    *reinterpret_cast<u32x2*>(out + kRopeDim / 2 + 4 * k) = rb;
   }
 }
 
@@ -213,7 +257,7 @@ hipError_t launch_qkv_a_rows(void* qkv, int64_t qkvs, int32_t q_rank, const void
 hipError_t launch_q_rope(const void* q, int64_t qst, int64_t qsh, int32_t tokens, int32_t heads, const int32_t* pos,
                          const float* cos_sin, int32_t max_pos, int32_t interleaved, void* pe, int64_t pst, int64_t psh,
                          void* nope, int64_t nst, int64_t nsh, hipStream_t stream) {
-  const int64_t items = (int64_t)tokens * heads;
+  const int64_t items = (int64_t)tokens * ((heads + kQRopeHeads - 1) / kQRopeHeads);
   if (items == 0) return hipSuccess;
   hipLaunchKernelGGL(q_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, (const __bf16*)q, qst,
                      qsh, tokens, heads, pos, cos_sin, max_pos, interleaved, (__bf16*)pe, pst, psh, (__bf16*)nope,

@@ -100,6 +100,25 @@ def test_q_rope_in_place_prefill_layout():
                                **TOL)
 
 
+@pytest.mark.parametrize("heads,interleaved", [(8, False), (20, True), (20, False), (128, True)])
+def test_q_rope_head_counts(heads, interleaved):
+    """Head counts that do not fill the kernel's 8-head groups (a tensor-parallel shard), both pair
+    layouts, in place: the nope dims and the padding past the last head stay untouched."""
+    T = 37
+    gen = torch.Generator().manual_seed(heads)
+    cache = rope_cos_sin_cache(64, MAX_POS, 50000.0, YARN).to(DEV)
+    wide = _bf16((T, heads + 1, 192), gen)
+    ref = wide.clone()
+    q = wide[:, :heads]
+    pos = torch.randint(0, MAX_POS, (T,), generator=gen, dtype=torch.int32).to(DEV)
+    lib.q_rope(q, pos, cache, interleaved, q[..., 128:])
+    torch.cuda.synchronize()
+    assert torch.equal(wide[:, heads], ref[:, heads]) and torch.equal(wide[..., :128], ref[..., :128])
+    inv, amp = RL.rope_inv_freq(64, 50000.0, dict(YARN))
+    torch.testing.assert_close(q[..., 128:].double().cpu(),
+                               RL.rope(ref[:, :heads, 128:].double().cpu(), pos.cpu(), inv, amp, interleaved), **TOL)
+
+
 def test_qkv_a_rows_equals_the_separate_ops():
     """The fused q_a / kv_a rows kernel gives the separate RMSNorm and latent-row kernels' output
     bit for bit (same arithmetic in the same order)."""
