@@ -238,6 +238,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
   int n_issued = 0;
   bool iss_valid = true;
   auto prologue = [&]() {
+    if constexpr (nparts == 0) return;  // a role without DMA parts keeps no issue cursor
     for (int s = 0; s < kWAhead && iss_valid; ++s) {
       issue(iss, n_issued++);
       iss_valid = advance(iss);
@@ -299,7 +300,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
       cs = piece_cur;
       iss = piece_cur;
       j = piece_j;
-      n_issued = piece_j;
+      n_issued = nparts > 0 ? piece_j : 0;
       iss_kv = piece_kv;
       comp_kv = piece_kv;
       iss_valid = true;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     if (prev_kv && prev_end) attempt = 0;
 
     constexpr bool kLate = kScore ? kWScoreLate : kWOutLate;
-    if (iss_valid && !kLate) {
+    if (nparts > 0 && iss_valid && !kLate) {
       issue(iss, n_issued++);
       iss_valid = advance(iss);
     }
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
       }
     }
 
-    if (kLate && iss_valid) {  // this step's DMA after the work
+    if (nparts > 0 && kLate && iss_valid) {  // this step's DMA after the work
       issue(iss, n_issued++);
       iss_valid = advance(iss);
     }
