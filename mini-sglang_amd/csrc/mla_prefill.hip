@@ -7,11 +7,13 @@
 //
 // One CTA per (request, 256 query rows, head); 4 waves x 64 query rows (two
 // 32-row sub-blocks), one wave per SIMD.
-//  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 7-stage
+//  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 6-stage
 //    LDS ring filled by 16-byte DMA loads. K rows (384 B) are stored with the
-//    16-byte chunk index XOR (token & 7) inside each 8-chunk group, V rows
-//    (256 B) with XOR 2 * (token & 3): the K operand reads and the transposing
-//    V reads are then bank-conflict free.
+//    16-byte chunk index XOR ((token >> 1) & 7) inside each 8-chunk group, V rows
+//    (256 B) with XOR 4 * (token & 3): the K operand reads (ds_read_b128) and the
+//    transposing V reads (ds_read_b64_tr_b16) are then bank-conflict free, as
+//    rocprof's SQ_LDS_BANK_CONFLICT reads them on this part (XOR (token & 7) and
+//    XOR 2 * (token & 3) leave both 2-way conflicted).
 //  * S^T[32 keys x 32 queries] = K . Q^T and O^T[128 dims x 32 queries] +=
 //    V^T . P^T on 32x32x16 bf16 MFMA; the queries stay in accumulation
 //    registers as the B operand, O in accumulation registers; each K and V^T
@@ -81,8 +83,8 @@ __device__ __forceinline__ int wave_sum(int v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
   return v;
 }
-__device__ __forceinline__ int kswz(int c, int t) { return (c & ~7) | ((c & 7) ^ (t & 7)); }
-__device__ __forceinline__ int vswz(int c, int t) { return c ^ (2 * (t & 3)); }
+__device__ __forceinline__ int kswz(int c, int t) { return (c & ~7) | ((c & 7) ^ ((t >> 1) & 7)); }
+__device__ __forceinline__ int vswz(int c, int t) { return c ^ (4 * (t & 3)); }
 // max / sum of a lane's value with lane ^ 32 (v_permlane32_swap, no LDS traffic)
 __device__ __forceinline__ float max_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -344,14 +346,13 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   for (int r = 0; r < 4; ++r) k_off[r] = c32 * kPKRowBytes + kswz(2 * r + g32, c32) * 16;
   // V^T operand: 16-lane group gq = lane / 16 covers dims 16(gq & 1) .. +16 of a 32-dim block and
   // the key quarter vh = gq >> 1; lane a16 reads token 4vh + (a16 >> 2) (+ 16 ksp + 8 second), dims
-  // 4(a16 & 3) .. +4; chunk 4db + y (y < 4) is stored at (4db + y) ^ 2vt
+  // 4(a16 & 3) .. +4; chunk 4db + y (y < 4) of token t is stored at 4(db ^ (t & 3)) + y
   const int gq = lane >> 4, a16 = lane & 15, vh = gq >> 1, vt = a16 >> 2;
-  int v_off[2];
+  int v_off[4];
   {
     const int y = 2 * (gq & 1) + ((a16 & 3) >> 1);
-    const int z = y ^ (2 * vt);
 #pragma unroll
-    for (int d = 0; d < 2; ++d) v_off[d] = (4 * vh + vt) * kPVRowBytes + ((4 * d) ^ z) * 16 + (a16 & 1) * 8;
+    for (int db = 0; db < 4; ++db) v_off[db] = (4 * vh + vt) * kPVRowBytes + (4 * (db ^ vt) + y) * 16 + (a16 & 1) * 8;
   }
   // K operand ks of the stage at LDS byte offset `kt`
   auto kread = [&](int kt, int ks) __attribute__((always_inline)) {
@@ -362,8 +363,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // k order (keys 16ksp + 8e + 4g32 + (0..3), e = 0, 1) matches the lanes' P^T values
   auto vop = [&](int kt, int st) __attribute__((always_inline)) {
     const int db = st >> 1, ksp = st & 1;
-    const MLA_LDS char* base = (const MLA_LDS char*)smem + kt + kPKBytes + v_off[db & 1] + 128 * (db >> 1) +
-                               16 * ksp * kPVRowBytes;
+    const MLA_LDS char* base = (const MLA_LDS char*)smem + kt + kPKBytes + v_off[db] + 16 * ksp * kPVRowBytes;
     const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)base);
     const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MLA_LDS bf16x4*)(base + 8 * kPVRowBytes));
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
