@@ -96,6 +96,33 @@ def test_decode_tensor_parallel_head_counts(heads, ps):
     torch.testing.assert_close(wide_lse[:, :heads].cpu(), lse_ref, **LSE_TOL)
 
 
+@pytest.mark.parametrize("heads,ps,num_ctas", [(128, 32, 64), (192, 64, 7), (256, 128, 256)])
+def test_decode_whole_head_groups(heads, ps, num_ctas):
+    """Multiples of 64 heads on pages of >= 32 tokens: every 64-head group runs the warp-specialized
+    kernel with its partials in its own workspace block; checked against the oracle, and the split
+    step + merge entry points against the one-call entry point bit for bit."""
+    print(f"[decode groups] heads={heads} ps={ps} ctas={num_ctas}", flush=True)
+    case = make_decode_case(5, heads, ps, lens=[1, 700, 2049, 64, 4000], seed=heads + ps)
+    check_case(case, num_ctas)
+    B = len(case.lens)
+    plan_np, slots = lib.decode_plan(case.lens, ps, num_ctas)
+    plan = torch.from_numpy(plan_np).to(DEV)
+    q, kv, pt, sl = case.q.to(DEV), case.kv_pool.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV)
+    outs = []
+    for two_step in (False, True):
+        ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.float32, device=DEV)
+        ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
+        out = torch.empty((B, heads, 512), dtype=torch.bfloat16, device=DEV)
+        lse = torch.empty((B, heads), dtype=torch.float32, device=DEV)
+        lib.mla_decode(q, kv, pt, sl, plan, num_ctas, ws_o, ws_lse, R.DEFAULT_SCALE, out, lse, split_only=two_step)
+        if two_step:
+            lib.mla_decode_merge(ws_o, ws_lse, plan[num_ctas * 4 :], out, lse, single_piece_final=True)
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), lse.cpu()))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("num_ctas", [256, 8])
 def test_decode_many_short_requests(num_ctas):
     """1024 requests of 0..200 tokens: at 8 CTAs each CTA's range holds the plan's maximum of 128
