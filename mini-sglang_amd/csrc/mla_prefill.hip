@@ -5,19 +5,20 @@
 // [.., H, 192] has them adjacent; the latent-decompression scratch keeps one rope copy per token,
 // shared by all heads, after the heads' [k_nope | v] blocks).
 //
-// One CTA per (request, 256 query rows, head); 4 waves x 64 query rows (two
-// 32-row sub-blocks), one wave per SIMD.
+// One CTA per (request, 256 query rows, head); 8 waves x 32 query rows, two waves per SIMD (the
+// kernel is a template on QS, the 32-row query sub-blocks per wave; QS = 2, 4 waves x 64 rows with
+// one wave per SIMD, measures the same and is kept buildable).
 //  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 6-stage
-//    LDS ring filled by 16-byte DMA loads. K rows (384 B) are stored with the
+//    LDS ring filled by 16-byte DMA loads: waves 0-3 load the K tile, waves 4-7 the V tile (one
+//    wave of each per SIMD). K rows (384 B) are stored with the
 //    16-byte chunk index XOR ((token >> 1) & 7) inside each 8-chunk group, V rows
 //    (256 B) with XOR 4 * (token & 3): the K operand reads (ds_read_b128) and the
 //    transposing V reads (ds_read_b64_tr_b16) are then bank-conflict free, as
 //    rocprof's SQ_LDS_BANK_CONFLICT reads them on this part (XOR (token & 7) and
 //    XOR 2 * (token & 3) leave both 2-way conflicted).
 //  * S^T[32 keys x 32 queries] = K . Q^T and O^T[128 dims x 32 queries] +=
-//    V^T . P^T on 32x32x16 bf16 MFMA; the queries stay in accumulation
-//    registers as the B operand, O in accumulation registers; each K and V^T
-//    read feeds both sub-blocks.
+//    V^T . P^T on 32x32x16 bf16 MFMA; queries (the B operand) and O stay in
+//    registers for the whole kernel (216 VGPRs with QS = 1).
 //  * Software pipeline over the stages: step j issues the value MFMAs of stage
 //    j-1 and the score MFMAs of stage j+1 while the vector ALU runs the online
 //    softmax of stage j, the two instruction streams interleaved slot by slot
@@ -39,38 +40,48 @@ namespace {
 
 typedef float f32x16_t __attribute__((__vector_size__(64)));
 
-constexpr int kPWaves = 4;
-constexpr int kPRowsPerWave = kPrefillRows / kPWaves;  // 64
 constexpr int kPStage = 32;                             // keys per stage
 constexpr int kPKRowBytes = kPrefillQkDim * 2;          // 384
 constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
 constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
 constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
 constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
-constexpr int kPStages = 6;  // ring stages; the loop over the steps is unrolled by this
-constexpr int kPKDma = kPKBytes / 1024 / kPWaves;  // 3 wave-wide DMA loads per wave
-constexpr int kPVDma = kPVBytes / 1024 / kPWaves;  // 2
-constexpr int kPDma = kPKDma + kPVDma;             // 5
+constexpr int kPStages = 6;  // ring stages
+// the loop over the steps is unrolled by this: whole rounds of the ring, and an even count (the
+// score and numerator registers alternate by step parity)
+constexpr int kPUnroll = kPStages % 2 == 0 ? kPStages : 2 * kPStages;
+// Wave-wide 1 KiB DMA loads of a stage: 12 of the K tile and 8 of the V tile; load i of a tile
+// lands at i KiB. With QS = 2 (4 waves) wave w issues K loads w + 4k (k < 3) and V loads w + 4k
+// (k < 2); with QS = 1 (8 waves) waves 0-3 issue the K loads (w + 4k, k < 3) and waves 4-7 the V
+// loads ((w - 4) + 4k, k < 2).
+constexpr int kPKDma = 3;  // K loads of a wave that issues K loads
+constexpr int kPVDma = 2;  // V loads of a wave that issues V loads
 constexpr int kPMaxGroups = 1024;  // stage sources of a CTA staged in LDS (else computed per stage)
 
-// ---- the softmax of one stage as a list of micro-operations, spread over the 40 MFMA slots of a
+// ---- the softmax of one stage as a list of micro-operations, spread over the MFMA slots of a
 // pipelined step in proportion to their cost (~4-cycle units; next to running MFMAs a vector
-// instruction costs ~8 cycles and exp2 ~11). For u in [0, 48): k = u / 6, r = u % 6:
-//   r = 0, 1 -> exp2 of score 2k + r of sub-block 0 against the row reference; r = 2, 3 -> the
-//   same for sub-block 1; r = 4, 5 -> sub-block r - 4: add the pair to the row sum and pack it to
-//   bf16. No exp2 result is used by the next instruction (that would cost a wait state).
-constexpr int kSlots = 40;  // 16 value MFMAs + 24 score MFMAs
-constexpr int kUops = 48;
-constexpr int uop_weight(int u) { return u % 6 < 4 ? 5 : 6; }
-constexpr int uop_total() {
+// instruction costs ~8 cycles and exp2 ~11). QS = query sub-blocks of 32 rows per wave: 1 (8 waves
+// of 32 rows, two per SIMD) or 2 (4 waves of 64 rows, one per SIMD). A step has 8 QS value MFMAs
+// + 12 QS score MFMAs (its slots) and 24 QS softmax micro-ops: for u = 3 QS k + r (pair k of a
+// lane's 16 scores), r < 2 QS is the exp2 of score 2k + r % 2 of sub-block r / 2 against the row
+// reference, r >= 2 QS adds sub-block r - 2 QS's pair to the row sum and packs it to bf16. No exp2
+// result is used by the next instruction (that would cost a wait state).
+template <int QS> constexpr int kSlots = 20 * QS;
+// LDS operand reads run ahead of their MFMAs: K operand ks + kAK is read in the slot of K operand
+// ks, V^T operand st + kAV in the slot of V^T operand st (the first kAV by the step before)
+constexpr int kAK = 4, kAV = 3;
+static_assert(kAK >= 3 && kAK <= 8 && kAV >= 1 && kAV <= 12, "read-ahead outside the step's slots");
+template <int QS> constexpr int kUops = 24 * QS;
+template <int QS> constexpr int uop_weight(int u) { return u % (3 * QS) < 2 * QS ? 5 : 6; }
+template <int QS> constexpr int uop_total() {
   int t = 0;
-  for (int u = 0; u < kUops; ++u) t += uop_weight(u);
+  for (int u = 0; u < kUops<QS>; ++u) t += uop_weight<QS>(u);
   return t;
 }
-constexpr int uop_slot(int u) {
+template <int QS> constexpr int uop_slot(int u) {
   int t = 0;
-  for (int v = 0; v < u; ++v) t += uop_weight(v);
-  return t * kSlots / uop_total();
+  for (int v = 0; v < u; ++v) t += uop_weight<QS>(v);
+  return t * kSlots<QS> / uop_total<QS>();
 }
 // The row reference m (log2 domain) is the exact max of the wave's first stage and moves only when
 // a stage's numerators sum past 2^32 (a score 32 above m, in log2 units) or overflow: then that
@@ -95,22 +106,40 @@ __device__ __forceinline__ float sum_halves(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// S^T += K . Q^T with the query operand read straight from accumulation registers. A chain
-// accumulates in place; its first k-step starts from zero.
+// S^T += K . Q^T. A chain accumulates in place; its first k-step starts from zero. With QS = 2
+// the query operand is read straight from accumulation registers (the wave holds 512 registers
+// per lane, split evenly), through assembly the compiler's hazard tracking does not see; with
+// QS = 1 (256 per lane) everything lives in the vector registers and the compiler places the
+// MFMAs and their wait states.
+template <int QS>
 __device__ __forceinline__ void mfma_qk_first(f32x16_t& d, const bf16x8& k, const bf16x8& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "a"(q));
+  if constexpr (QS == 2) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "a"(q));
+  else d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k, q, f32x16_t{}, 0, 0, 0);
 }
+template <int QS>
 __device__ __forceinline__ void mfma_qk(f32x16_t& d, const bf16x8& k, const bf16x8& q) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "a"(q));
+  if constexpr (QS == 2) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "a"(q));
+  else d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k, q, d, 0, 0, 0);
+}
+// keeps an output block in its register file and its MFMA in its slot
+template <int QS>
+__device__ __forceinline__ void pin_o(f32x16_t& o) {
+  if constexpr (QS == 2) asm volatile("" : "+a"(o));
+  else asm volatile("" : "+v"(o));
 }
 // O^T += V^T . P^T (the compiler places O and tracks its hazards).
 __device__ __forceinline__ void mfma_pv(f32x16_t& o, const bf16x8& v, const u32x4& p) {
   o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, __builtin_bit_cast(bf16x8, p), o, 0, 0, 0);
 }
-// The score MFMAs are opaque to the compiler's hazard tracking: before the vector ALU reads their
-// results, wait out the pipeline (24 wait states >= what a 16-pass MFMA needs).
+// The assembly score MFMAs (QS = 2) are opaque to the compiler's hazard tracking: before the
+// vector ALU reads their results, wait out the pipeline (24 wait states >= what a 16-pass MFMA
+// needs).
 __device__ __forceinline__ void mfma_wait_scores(f32x16_t& a, f32x16_t& b) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
+template <int QS>
+__device__ __forceinline__ void mfma_wait_scores(f32x16_t (&s)[QS]) {
+  if constexpr (QS == 2) mfma_wait_scores(s[0], s[1]);
 }
 
 // Pin a vector-ALU result to its place in the instruction stream: the empty volatile asm is
@@ -130,9 +159,12 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-__global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams p) {
+template <int QS>
+__global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const PrefillParams p) {
+  constexpr int kPWaves = 8 / QS;
+  constexpr int kPRowsPerWave = 32 * QS;
   // the ring, then one stage-sized area that dummy DMA groups load into
-  __shared__ __attribute__((aligned(1024))) char smem[(kPStages + 1) * kPStageBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kPStages * kPStageBytes + 1024];
   __shared__ __attribute__((aligned(16))) uint32_t s_src[kPMaxGroups + 1][4];  // K and V source of stage g
 
   const int lane = threadIdx.x & 63;
@@ -211,9 +243,9 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 
   // ---- queries, loaded first so that their latency overlaps the page-table reads below:
   // qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
-  bf16x8 qf[2][12];
+  bf16x8 qf[QS][12];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const int row = row0 + 32 * qs + c32;
     const bool ok = row < E;
     const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)h * p.q_stride_h + 8 * g32;
@@ -224,7 +256,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // of dummy groups); a CTA with more stages than that computes each stage's source when it loads it
   const bool staged = nst <= kPMaxGroups;
   const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
-  for (int g = threadIdx.x; g <= n_defer; g += 256) {
+  for (int g = threadIdx.x; g <= n_defer; g += kPWaves * 64) {
     const int t0 = g < n_defer ? g * kPStage : 0;
     const uint32_t pid = (uint32_t)min(max(p.page_table[(int64_t)b * p.pt_stride + (t0 >> p.log2_ps)], 0), p.num_pages - 1);
     const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
@@ -236,26 +268,41 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // ---- DMA of stage n (32 tokens of one page: page_size >= 64); rows past the last key load the
   // last key. LDS position s (16 bytes each) of the K tile holds token s / 24, chunk kswz(s % 24);
   // of the V tile token s / 16, chunk vswz(s % 16).
+  const int wq = wave & 3;
+  const bool k_wave = QS == 2 || wave < 4;  // this wave issues K loads wq + 4k
+  const bool v_wave = QS == 2 || wave >= 4;  // this wave issues V loads wq + 4k
+  constexpr int kPDmaMax = QS == 2 ? kPKDma + kPVDma : kPKDma;  // loads per wave, at most
   uint32_t koff[kPKDma], voff[kPVDma];
 #pragma unroll
   for (int k = 0; k < kPKDma; ++k) {
-    const int s = (wave + k * kPWaves) * 64 + lane, t = s / 24;
+    const int s = (wq + 4 * k) * 64 + lane, t = s / 24;
     koff[k] = (uint32_t)(t * krow_bytes) + kchunk_src(kswz(s - 24 * t, t));
   }
 #pragma unroll
   for (int k = 0; k < kPVDma; ++k) {
-    const int s = (wave + k * kPWaves) * 64 + lane, t = s >> 4;
+    const int s = (wq + 4 * k) * 64 + lane, t = s >> 4;
     voff[k] = (uint32_t)(t * vrow_bytes + vswz(s & 15, t) * 16);
   }
-  // DMA groups (5 loads per wave) are issued in order, real stages in stage order, stage n into
-  // ring slot n % kPStages. Every step issues exactly one group, one load at a time in its slots:
-  // the next stage when it is a full one with a staged source, otherwise a dummy group (the first
-  // stage again, into the dummy area), so that the slots carry no branches; a tail stage (and every
-  // stage of a CTA without staged sources) is issued at once, ahead of that dummy.
+  // DMA groups (a wave's loads of one stage: 5 with QS = 2; 3 or 2 with QS = 1) are issued in
+  // order, real stages in stage order, stage n into ring slot n % kPStages. Every step issues
+  // exactly one group, one load at a time in its slots: the next stage when it is a full one with a
+  // staged source, otherwise a dummy group (the first stage again, every load of it into one 1 KB
+  // area past the ring), so that the slots carry no branches; a tail stage (and every stage of a
+  // CTA without staged sources) is issued at once, ahead of that dummy.
+  // QS = 1: a wave's loads are all K or all V, so its slot work is one list: per-lane source
+  // offsets doff, the source from entry half src_sel of the stage's s_src row, the LDS destination
+  // tile_off into the stage (the V-only waves' third load is absent)
+  const uint32_t tile_off = k_wave || QS == 2 ? 0u : (uint32_t)kPKBytes;
+  const int src_sel = k_wave ? 0 : 8;
+  uint32_t doff[kPKDma];
+#pragma unroll
+  for (int d = 0; d < kPKDma; ++d) doff[d] = k_wave ? koff[d] : voff[d < kPVDma ? d : kPVDma - 1];
   int n_stages = 0, n_groups = 0;
   const uint32_t lds_dummy = lds0 + kPStages * kPStageBytes;
   int dma_idx = 0;       // s_src entry of the step's group
   uint32_t dma_m0w = 0;  // its LDS destination, this wave's first 1 KB
+  uint32_t dma_pst = 0;  // LDS distance of its successive loads (0 for a dummy group: every load of
+                         // a dummy group lands in the same 1 KB past the ring, which nothing reads)
   auto issue_now = [&]() __attribute__((always_inline)) {  // stage n_stages < nst, all loads now
     const int t0 = n_stages * kPStage;
     const int tlim = L - 1 - t0;
@@ -272,17 +319,21 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     // offsets are computed here and not kept in registers across the loop)
     int ln;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    if (k_wave) {
 #pragma unroll
-    for (int k = 0; k < kPKDma; ++k) {
-      const int s = (wave + k * kPWaves) * 64 + ln, t = s / 24;
-      const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes) + kchunk_src(kswz(s - 24 * t, t));
-      dma16_saddr(ksrc, o, st + (wave + k * kPWaves) * 1024);
+      for (int k = 0; k < kPKDma; ++k) {
+        const int s = (wq + 4 * k) * 64 + ln, t = s / 24;
+        const uint32_t o = (uint32_t)(min(t, tlim) * krow_bytes) + kchunk_src(kswz(s - 24 * t, t));
+        dma16_saddr(ksrc, o, st + (wq + 4 * k) * 1024);
+      }
     }
+    if (v_wave) {
 #pragma unroll
-    for (int k = 0; k < kPVDma; ++k) {
-      const int s = (wave + k * kPWaves) * 64 + ln, t = s >> 4;
-      const uint32_t o = (uint32_t)(min(t, tlim) * vrow_bytes + vswz(s & 15, t) * 16);
-      dma16_saddr(vsrc, o, st + kPKBytes + (wave + k * kPWaves) * 1024);
+      for (int k = 0; k < kPVDma; ++k) {
+        const int s = (wq + 4 * k) * 64 + ln, t = s >> 4;
+        const uint32_t o = (uint32_t)(min(t, tlim) * vrow_bytes + vswz(s & 15, t) * 16);
+        dma16_saddr(vsrc, o, st + kPKBytes + (wq + 4 * k) * 1024);
+      }
     }
     ++n_stages;
     ++n_groups;
@@ -294,48 +345,69 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     const bool real = n_groups < n_defer;
     dma_idx = real ? n_groups : n_defer;
     const uint32_t slot = SL >= 0 ? (uint32_t)SL * kPStageBytes : (uint32_t)(n_groups % kPStages) * kPStageBytes;
-    dma_m0w = (real ? lds0 + slot : lds_dummy) + wave * 1024;
+    dma_m0w = real ? lds0 + slot + wq * 1024 + tile_off : lds_dummy;
+    dma_pst = real ? 4 * 1024 : 0;
     if (real) ++n_stages;
     else if (__builtin_expect(n_stages < nst, 0)) issue_now();
     ++n_groups;
   };
   // slot work of the step's group: part 0 reads its sources (in the step, so the compiler waits
-  // for that LDS read alone), parts 1..5 issue the loads
+  // for that LDS read alone), parts 1..kPDmaMax issue the loads (a V-only wave has no part 3)
   u32x4 dma_e;
+  u32x2 dma_e1;
   const char* dma_k = kbase;
   const char* dma_v = vbase;
   auto dma_part = [&](int k) __attribute__((always_inline)) {
-    if (k == 0) {
-      dma_e = *reinterpret_cast<const MLA_LDS u32x4*>((const MLA_LDS char*)s_src + 16 * dma_idx);
-      return;
+    if constexpr (QS == 2) {
+      if (k == 0) {
+        dma_e = *reinterpret_cast<const MLA_LDS u32x4*>((const MLA_LDS char*)s_src + 16 * dma_idx);
+        return;
+      }
+      if (k == 1) {
+        dma_k = uniform_ptr(dma_e[0], dma_e[1]);
+        dma_v = uniform_ptr(dma_e[2], dma_e[3]);
+      }
+      const int d = k - 1;
+      if (d < kPKDma) dma16_saddr(dma_k, koff[d], dma_m0w + d * dma_pst);
+      else dma16_saddr(dma_v, voff[d - kPKDma], dma_m0w + (dma_pst != 0 ? kPKBytes : 0) + (d - kPKDma) * dma_pst);
+    } else {
+      if (k == 0) {
+        dma_e1 = *reinterpret_cast<const MLA_LDS u32x2*>((const MLA_LDS char*)s_src + 16 * dma_idx + src_sel);
+        return;
+      }
+      if (k == 1) dma_k = uniform_ptr(dma_e1[0], dma_e1[1]);
+      const int d = k - 1;
+      if (d < kPVDma || k_wave) dma16_saddr(dma_k, doff[d], dma_m0w + d * dma_pst);
     }
-    if (k == 1) {
-      dma_k = uniform_ptr(dma_e[0], dma_e[1]);
-      dma_v = uniform_ptr(dma_e[2], dma_e[3]);
-    }
-    const int d = k - 1;
-    if (d < kPKDma) dma16_saddr(dma_k, koff[d], dma_m0w + d * kPWaves * 1024);
-    else dma16_saddr(dma_v, voff[d - kPKDma], dma_m0w + kPKBytes + (d - kPKDma) * kPWaves * 1024);
   };
   // all loads of the step's group at once (a wave without work in the step, and the groups before
   // the first step)
   auto group_now = [&](auto slot_c) __attribute__((always_inline)) {
     group_setup(slot_c);
 #pragma unroll
-    for (int k = 0; k <= kPDma; ++k) dma_part(k);
+    for (int k = 0; k <= kPDmaMax; ++k) dma_part(k);
   };
   // stage n + 1 has landed for every wave, and every wave is done with step n - 1 (so the stage
   // that step finished with may be refilled): every step issues exactly one group, so
-  // kPStages - 4 groups follow stage n + 1's and at most 5 (kPStages - 4) loads may still be in flight
+  // kPStages - 4 groups follow stage n + 1's and at most (loads per group) (kPStages - 4) loads may
+  // still be in flight
   auto step_sync = [&]() __attribute__((always_inline)) {
-    wait_vmcnt<kPDma * (kPStages - 4)>();
+    if (QS == 2) wait_vmcnt<(kPKDma + kPVDma) * (kPStages - 4)>();
+    else if (k_wave) wait_vmcnt<kPKDma * (kPStages - 4)>();
+    else wait_vmcnt<kPVDma * (kPStages - 4)>();
     __builtin_amdgcn_s_barrier();
   };
-  // the queries stay in accumulation registers for the whole kernel (the score MFMAs read them there)
+  // the queries stay in registers for the whole kernel (with QS = 2 in the accumulation registers,
+  // which the score MFMAs read) and have landed here, before the first loads of the ring: the DMA
+  // loads are inline assembly the compiler does not count, so a wait for the queries later on
+  // would be a full vmcnt(0)
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs)
+  for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-    for (int ks = 0; ks < 12; ++ks) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
+    for (int ks = 0; ks < 12; ++ks) {
+      if constexpr (QS == 2) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
+      else asm volatile("" : "+v"(qf[qs][ks]));
+    }
 
   for (int g = 0; g < kPStages - 3; ++g) group_now(ic<-1>{});
 
@@ -369,38 +441,40 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
-  f32x16_t O[4][2];
+  f32x16_t O[4][QS];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) O[db][0] = O[db][1] = f32x16_t{};
-  float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-  f32x16_t sc[2][2];  // [parity][qs]: scores of the stage being softmaxed / being computed
-  u32x4 pb[2][2][2];  // [parity][qs][ksp]: bf16 numerators P^T
-  bf16x8 vb[4];       // V^T operands (the first three of a step are read by the step before)
-  bf16x8 kb[5];       // K operands in flight
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) O[db][qs] = f32x16_t{};
+  float m_ref[QS], l_run[QS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) m_ref[qs] = -INFINITY, l_run[qs] = 0.f;
+  f32x16_t sc[2][QS];  // [parity][qs]: scores of the stage being softmaxed / being computed
+  u32x4 pb[2][QS][2];  // [parity][qs][ksp]: bf16 numerators P^T
+  bf16x8 vb[kAV + 1];  // V^T operands in flight (the first kAV of a step are read by the step before)
+  bf16x8 kb[kAK + 1];  // K operands in flight
 
   // ---- scores of stage 0 (before the first pipelined step)
-  auto qk_plain = [&](f32x16_t (&dst)[2], int kt) __attribute__((always_inline)) {
+  auto qk_plain = [&](f32x16_t (&dst)[QS], int kt) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) kb[r] = kread(kt, r);
 #pragma unroll
     for (int ks = 0; ks < 12; ++ks) {
       const bf16x8 a = kb[ks & 3];
       if (ks + 4 < 12) kb[ks & 3] = kread(kt, ks + 4);
-      if (ks == 0) {
-        mfma_qk_first(dst[0], a, qf[0][0]);
-        mfma_qk_first(dst[1], a, qf[1][0]);
-      } else {
-        mfma_qk(dst[0], a, qf[0][ks]);
-        mfma_qk(dst[1], a, qf[1][ks]);
+#pragma unroll
+      for (int qs = 0; qs < QS; ++qs) {
+        if (ks == 0) mfma_qk_first<QS>(dst[qs], a, qf[qs][0]);
+        else mfma_qk<QS>(dst[qs], a, qf[qs][ks]);
       }
     }
   };
   // causal mask of stage j's scores (stages that reach past the wave's first query); all == true
   // masks every score
-  auto mask_scores = [&](f32x16_t (&sv)[2], int j, bool all) __attribute__((always_inline)) {
-    mfma_wait_scores(sv[0], sv[1]);
+  auto mask_scores = [&](f32x16_t (&sv)[QS], int j, bool all) __attribute__((always_inline)) {
+    mfma_wait_scores<QS>(sv);
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
       // key kfirst + 8(i/4) + 4 g32 + i%4 follows query P + row0 + 32qs + c32 when
       // 8(i/4) + i%4 > lim, lim = P + row0 + 32qs + c32 - kfirst - 4 g32
       const int lim = all ? -1 : P + row0 + 32 * qs + c32 - j * kPStage - 4 * g32;
@@ -409,12 +483,14 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         if (8 * (i >> 2) + (i & 3) > lim) sv[qs][i] = -INFINITY;
     }
   };
-  float negm[2] = {0.f, 0.f};  // -reference per sub-block (log2 domain)
-  // reference of the wave's first stage: its exact row max
-  auto init_ref = [&](f32x16_t (&sv)[2]) __attribute__((always_inline)) {
-    mfma_wait_scores(sv[0], sv[1]);
+  float negm[QS];  // -reference per sub-block (log2 domain)
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) negm[qs] = 0.f;
+  // reference of the wave's first stage: its exact row max
+  auto init_ref = [&](f32x16_t (&sv)[QS]) __attribute__((always_inline)) {
+    mfma_wait_scores<QS>(sv);
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
       float m = sv[qs][0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) m = fmaxf(m, sv[qs][i]);
@@ -425,10 +501,10 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
   // stage j again, its reference raised to its exact max (rare): from its raw (masked) scores,
   // which the pipelined step keeps; O and l (which hold the stages before it) rescaled; numerators
   // and their sum redone
-  auto redo_stage = [&](f32x16_t (&sv)[2], u32x4 (&dst)[2][2], float (&l_step)[2]) __attribute__((always_inline)) {
-    float fr[2];
+  auto redo_stage = [&](f32x16_t (&sv)[QS], u32x4 (&dst)[QS][2], float (&l_step)[QS]) __attribute__((always_inline)) {
+    float fr[QS];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
       float m = sv[qs][0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) m = fmaxf(m, sv[qs][i]);
@@ -451,42 +527,42 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
+      for (int qs = 0; qs < QS; ++qs) {
         O[db][qs] *= fr[qs];
-        asm volatile("" : "+a"(O[db][qs]));  // O stays in the accumulation registers
+        pin_o<QS>(O[db][qs]);
         __builtin_amdgcn_sched_barrier(0);
       }
   };
 
-  // ---- pipelined step j: value MFMAs of stage j - 1 (slots 0..15), score MFMAs of stage j + 1
-  // (slots 16..39), softmax of stage j spread over all slots; one MFMA per slot, the order pinned
-  // by scheduling barriers. V^T operands 0..2 are read by the step before (slots 36..38), 3..7 in
-  // slots 0..8 (six slots ahead); K operand ks is read in slot 8 + 2ks (eight slots ahead).
-  // ring offsets of stages j - 1 (j for j = 0), j and j + 1
+  // ---- pipelined step j: value MFMAs of stage j - 1 (slots 0 .. 8 QS - 1), score MFMAs of stage
+  // j + 1 (the next 12 QS slots), softmax of stage j spread over all slots; one MFMA per slot, the
+  // order pinned by scheduling barriers; LDS operand reads kAK / kAV operands ahead.
   // step j = j0 + U with j0 a multiple of kPStages: ring slots (U - 1, U, U + 1) % kPStages hold
   // stages j - 1, j and j + 1, and the step loads stage j + kPStages - 2 into slot (U - 2) % kPStages
   auto step_fast = [&](auto par_c, auto u_c) __attribute__((always_inline)) {
     constexpr int U = decltype(u_c)::value;
     constexpr int slot_prev = (U + kPStages - 1) % kPStages * kPStageBytes;
-    constexpr int slot_cur = U * kPStageBytes;
+    constexpr int slot_cur = U % kPStages * kPStageBytes;
     constexpr int slot_next = (U + 1) % kPStages * kPStageBytes;
     constexpr int par = decltype(par_c)::value;
-    f32x16_t(&scs)[2] = sc[par];
-    f32x16_t(&scn)[2] = sc[par ^ 1];
-    u32x4(&pbw)[2][2] = pb[par];
-    const u32x4(&pbr)[2][2] = pb[par ^ 1];
+    constexpr int NS = kSlots<QS>;
+    constexpr int kDmaPeriod = NS / kPDmaMax;  // DMA part p (1..) goes to slot kDmaPeriod (p - 1) + 3
+    f32x16_t(&scs)[QS] = sc[par];
+    f32x16_t(&scn)[QS] = sc[par ^ 1];
+    u32x4(&pbw)[QS][2] = pb[par];
+    const u32x4(&pbr)[QS][2] = pb[par ^ 1];
     const int kt = slot_next, vtile = slot_prev;
-    float l_step[2], ev[2][2];  // ev: the numerators of the pair being packed (raw scores stay)
+    float l_step[QS], ev[QS][2];  // ev: the numerators of the pair being packed (raw scores stay)
     float l_step_max;
     auto uop = [&](auto u_c) __attribute__((always_inline)) {
       constexpr int u = decltype(u_c)::value;
-      constexpr int k = u / 6, r = u % 6;
-      if constexpr (r < 4) {
+      constexpr int k = u / (3 * QS), r = u % (3 * QS);
+      if constexpr (r < 2 * QS) {
         constexpr int qs = r >> 1, e = r & 1;
         ev[qs][e] = __builtin_amdgcn_exp2f(fmaf(scs[qs][2 * k + e], p.scale_log2, negm[qs]));
         pin(ev[qs][e]);
       } else {
-        constexpr int qs = r - 4;
+        constexpr int qs = r - 2 * QS;
         l_step[qs] = k == 0 ? ev[qs][0] + ev[qs][1] : l_step[qs] + ev[qs][0] + ev[qs][1];
         uint32_t w = pack_bf16x2(ev[qs][0], ev[qs][1]);
         pin(l_step[qs]);
@@ -494,41 +570,39 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
         pbw[qs][k >> 2][k & 3] = w;
       }
     };
-    static_for<kSlots>([&](auto s_c) __attribute__((always_inline)) {
+    static_for<NS>([&](auto s_c) __attribute__((always_inline)) {
       constexpr int s = decltype(s_c)::value;
-      if constexpr (s == 0) mfma_wait_scores(scs[0], scs[1]);
-      if constexpr (s < 16) {
-        constexpr int st = s >> 1, qs = s & 1;
-        mfma_pv(O[st >> 1][qs], vb[st & 3], pbr[qs][st & 1]);
-        asm volatile("" : "+a"(O[st >> 1][qs]));  // keeps the value MFMA in its slot
+      if constexpr (s == 0) mfma_wait_scores<QS>(scs);
+      if constexpr (s < 8 * QS) {
+        constexpr int st = s / QS, qs = s % QS;
+        mfma_pv(O[st >> 1][qs], vb[st % (kAV + 1)], pbr[qs][st & 1]);
+        pin_o<QS>(O[st >> 1][qs]);
       } else {
-        constexpr int ks = (s - 16) >> 1, qs = s & 1;
-        if constexpr (ks == 0) mfma_qk_first(scn[qs], kb[0], qf[qs][0]);
-        else mfma_qk(scn[qs], kb[ks % 5], qf[qs][ks]);
+        constexpr int ks = (s - 8 * QS) / QS, qs = s % QS;
+        if constexpr (ks == 0) mfma_qk_first<QS>(scn[qs], kb[0], qf[qs][0]);
+        else mfma_qk<QS>(scn[qs], kb[ks % (kAK + 1)], qf[qs][ks]);
       }
       if constexpr (s == 0) dma_part(0);  // the stage refill, spread over the step
-      if constexpr (s % 8 == 3) dma_part(s / 8 + 1);
-      if constexpr (s < 10 && (s & 1) == 0) {
-        constexpr int st = (s >> 1) + 3;
-        vb[st & 3] = vop(vtile, st);
+      if constexpr (s % kDmaPeriod == 3 && s / kDmaPeriod < kPDmaMax) dma_part(s / kDmaPeriod + 1);
+      if constexpr (s % QS == 0) {  // operand reads, in units of one MFMA per sub-block
+        constexpr int a = s / QS;
+        constexpr int st = a + kAV, stn = a + kAV - 20, ks = a - 8 + kAK;
+        if constexpr (st < 8) vb[st % (kAV + 1)] = vop(vtile, st);
+        if constexpr (stn >= 0 && stn < kAV) vb[stn % (kAV + 1)] = vop(slot_cur, stn);  // the next step's
+        if constexpr (ks >= 0 && ks < 12) kb[ks % (kAK + 1)] = kread(kt, ks);
       }
-      if constexpr (s >= 8 && s <= 30 && (s & 1) == 0) {
-        constexpr int ks = (s - 8) >> 1;
-        kb[ks % 5] = kread(kt, ks);
-      }
-      if constexpr (s >= 36 && s <= 38) vb[s - 36] = vop(slot_cur, s - 36);  // for the next step
-      static_for<kUops>([&](auto u_c) __attribute__((always_inline)) {
-        if constexpr (uop_slot(decltype(u_c)::value) == s) uop(u_c);
+      static_for<kUops<QS>>([&](auto u_c) __attribute__((always_inline)) {
+        if constexpr (uop_slot<QS>(decltype(u_c)::value) == s) uop(u_c);
       });
       __builtin_amdgcn_sched_barrier(0);
     });
     // any lane's sum at 2^32 or more, or infinite: one compare into a lane mask, no reduction
     uint64_t big;
     asm volatile("v_max_f32 %1, %2, %3\n\tv_cmp_le_f32_e64 %0, %4, %1"
-                 : "=s"(big), "=&v"(l_step_max) : "v"(l_step[0]), "v"(l_step[1]), "v"(kPLazyMax));
+                 : "=s"(big), "=&v"(l_step_max) : "v"(l_step[0]), "v"(l_step[QS - 1]), "v"(kPLazyMax));
     if (big != 0) redo_stage(scs, pbw, l_step);
-    l_run[0] += l_step[0];
-    l_run[1] += l_step[1];
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) l_run[qs] += l_step[qs];
   };
 
   // step j <= W of a wave: the pipelined step. At j = 0 the value pass adds zero numerators (V of
@@ -539,6 +613,7 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     constexpr int U = decltype(u_c)::value;
     constexpr int par = U & 1;
     using slot_c = ic<(U + kPStages - 2) % kPStages>;
+    if (j > nst) return;  // uniform over the CTA: past the last stage
     step_sync();
     if (__builtin_expect(j <= W && W > 0, 1)) {
       group_setup(slot_c{});
@@ -550,25 +625,25 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
     }
   };
 
-  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier), rounded up to
-  // whole rounds of the ring (the steps past nst only load dummy groups). A wave without rows has
-  // W = 0 and only takes the barriers and loads its groups.
+  // step -1: scores of stage 0; then steps 0..nst (every wave takes every barrier; the unrolled
+  // steps past nst are skipped). A wave without rows has W = 0 and only takes the barriers and
+  // loads its groups.
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
+  for (int qs = 0; qs < QS; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
   step_sync();
   group_now(ic<-1>{});
   if (W > 0) {
     qk_plain(sc[0], 0);
-    vb[0] = vop(0, 0);
-    vb[1] = vop(0, 1);
-    vb[2] = vop(0, 2);
+#pragma unroll
+    for (int st = 0; st < kAV; ++st) vb[st] = vop(0, st);
   }
-  for (int j0 = 0; j0 <= nst; j0 += kPStages)
-    static_for<kPStages>([&](auto u_c) __attribute__((always_inline)) { step(u_c, j0 + decltype(u_c)::value); });
+  for (int j0 = 0; j0 <= nst; j0 += kPUnroll)
+    static_for<kPUnroll>([&](auto u_c) __attribute__((always_inline)) { step(u_c, j0 + decltype(u_c)::value); });
+  wait_vmcnt<0>();  // the last groups' loads into LDS have landed before the CTA ends
 
   // ---- finalise: lane holds query column c32 and dims 32db + 8(i/4) + 4*g32 + i%4
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     const int row = row0 + 32 * qs + c32;
     const float l_tot = sum_halves(l_run[qs]);
     if (row >= E || wave_rows == 0) continue;
@@ -591,11 +666,14 @@ __global__ __launch_bounds__(256, 1) void mla_prefill_kernel(const PrefillParams
 
 }  // namespace
 
+// query sub-blocks of 32 rows per wave: 1 (8 waves, two per SIMD) or 2 (4 waves, one per SIMD)
+constexpr int kPrefillQS = 1;
+
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream) {
   // upper bound on sum_b ceil(E_b / 256) over the batch, times the heads
   const int64_t items = ((int64_t)(total_q + kPrefillRows - 1) / kPrefillRows + p.batch) * p.heads;
   if (items <= 0) return hipSuccess;
-  hipLaunchKernelGGL(mla_prefill_kernel, dim3((unsigned)items), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(mla_prefill_kernel<kPrefillQS>, dim3((unsigned)items), dim3(8 / kPrefillQS * 64), 0, stream, p);
   return hipGetLastError();
 }
 
