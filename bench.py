@@ -130,6 +130,27 @@ def _cpu_baseline(case_gpu, runs: int = 10):
     }
 
 
+CLOCK_WARM_S = 0.3
+
+
+def _clock_warm(fn, seconds=CLOCK_WARM_S):
+    """Run ``fn(i)`` back to back for ``seconds`` of wall time before a timed region (untimed).
+
+    The GPU leaves its idle clocks over the first tens of milliseconds of load: per-launch HIP
+    events put the first 100 decode layer steps after idle at 126 us on average against ~91 us in
+    steady state, and the first prefill launches at 1.35-2.2 ms against ~1.22 ms. A timed region
+    that followed only a few warm-up steps would measure that ramp, not the kernels."""
+    import torch
+
+    end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < end:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def bench_decode(args):
     import torch
 
@@ -178,7 +199,9 @@ def bench_decode(args):
         return g
 
     with torch.cuda.stream(stream):
-        # ---- timed: exactly args.steps layer steps, eager launches on one stream
+        # ---- timed: exactly args.steps layer steps, eager launches on one stream, after the clock
+        # warm-up and args.warmup untimed steps
+        _clock_warm(layer)
         for i in range(args.warmup):
             layer(i)
         torch.cuda.synchronize()
@@ -318,6 +341,7 @@ def bench_prefill(args):
 
     steps = max(1, args.steps // 2)
     with torch.cuda.stream(stream):
+        _clock_warm(lambda i: layer())
         for _ in range(max(1, args.warmup // 2)):
             layer()
         torch.cuda.synchronize()
@@ -409,10 +433,12 @@ class _PrefillCall:
 
 
 def _time_device(fn, stream, steps, warmup):
-    """Mean device time (ms) of ``fn()`` over ``steps`` launches on ``stream`` (HIP events on that stream)."""
+    """Mean device time (ms) of ``fn()`` over ``steps`` launches on ``stream`` (HIP events on that stream),
+    after the clock warm-up and ``warmup`` untimed launches."""
     import torch
 
     with torch.cuda.stream(stream):
+        _clock_warm(lambda i: fn())
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()

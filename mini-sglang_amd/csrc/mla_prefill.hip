@@ -46,7 +46,13 @@ constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
 constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
 constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
 constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
-constexpr int kPStages = 6;  // ring stages
+// Steps between CTA barriers (1 or 2). Step j loads stage j + kPDist; a barrier step makes
+// stages up to j + kPSync visible to every wave, and the ring has kPSync - 1 more stages than one
+// barrier per step needs, so that a wave one step ahead of another never refills a stage the other
+// still reads.
+constexpr int kPSync = 2;
+constexpr int kPDist = 4;
+constexpr int kPStages = kPDist + 1 + kPSync;  // ring stages
 // the loop over the steps is unrolled by this: whole rounds of the ring, and an even count (the
 // score and numerator registers alternate by step parity)
 constexpr int kPUnroll = kPStages % 2 == 0 ? kPStages : 2 * kPStages;
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
     ++n_groups;
   };
   // the group of a step; slot_c: the ring slot of the group when it is a real one (step j loads
-  // stage j + kPStages - 2, the unrolled loop knows j % kPStages), or -1 to compute it
+  // stage j + kPDist, the unrolled loop knows j % kPStages), or -1 to compute it
   auto group_setup = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SL = decltype(slot_c)::value;
     const bool real = n_groups < n_defer;
@@ -387,16 +393,19 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
 #pragma unroll
     for (int k = 0; k <= kPDmaMax; ++k) dma_part(k);
   };
-  // stage n + 1 has landed for every wave, and every wave is done with step n - 1 (so the stage
-  // that step finished with may be refilled): every step issues exactly one group, so
-  // kPStages - 4 groups follow stage n + 1's and at most (loads per group) (kPStages - 4) loads may
-  // still be in flight
-  auto step_sync = [&]() __attribute__((always_inline)) {
-    if (QS == 2) wait_vmcnt<(kPKDma + kPVDma) * (kPStages - 4)>();
-    else if (k_wave) wait_vmcnt<kPKDma * (kPStages - 4)>();
-    else wait_vmcnt<kPVDma * (kPStages - 4)>();
+  // the stages before the last NG groups a wave issued have landed for every wave, and every wave
+  // is done with the steps before (so the stages they finished with may be refilled). Every step
+  // issues exactly one group (a step that loads a tail stage at once issues one more, which only
+  // makes the wait stricter), so at most (loads per group) NG loads may still be in flight.
+  auto sync_groups = [&](auto ng_c) __attribute__((always_inline)) {
+    constexpr int NG = decltype(ng_c)::value;
+    if (QS == 2) wait_vmcnt<(kPKDma + kPVDma) * NG>();
+    else if (k_wave) wait_vmcnt<kPKDma * NG>();
+    else wait_vmcnt<kPVDma * NG>();
     __builtin_amdgcn_s_barrier();
   };
+  // a barrier step n: stages n + 1 .. n + kPSync landed (kPDist - 1 - kPSync groups follow them)
+  auto step_sync = [&]() __attribute__((always_inline)) { sync_groups(ic<kPDist - 1 - kPSync>{}); };
   // the queries stay in registers for the whole kernel (with QS = 2 in the accumulation registers,
   // which the score MFMAs read) and have landed here, before the first loads of the ring: the DMA
   // loads are inline assembly the compiler does not count, so a wait for the queries later on
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
       else asm volatile("" : "+v"(qf[qs][ks]));
     }
 
-  for (int g = 0; g < kPStages - 3; ++g) group_now(ic<-1>{});
+  for (int g = 0; g < kPDist - 1; ++g) group_now(ic<-1>{});
 
   // ---- per-lane LDS read offsets
   // K operand of k-step ks = 4m + r: chunk 8m + 2r + g32 of key c32 at k_off[r] + 128m
@@ -538,7 +547,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   // j + 1 (the next 12 QS slots), softmax of stage j spread over all slots; one MFMA per slot, the
   // order pinned by scheduling barriers; LDS operand reads kAK / kAV operands ahead.
   // step j = j0 + U with j0 a multiple of kPStages: ring slots (U - 1, U, U + 1) % kPStages hold
-  // stages j - 1, j and j + 1, and the step loads stage j + kPStages - 2 into slot (U - 2) % kPStages
+  // stages j - 1, j and j + 1, and the step loads stage j + kPDist into slot (U + kPDist) % kPStages
   auto step_fast = [&](auto par_c, auto u_c) __attribute__((always_inline)) {
     constexpr int U = decltype(u_c)::value;
     constexpr int slot_prev = (U + kPStages - 1) % kPStages * kPStageBytes;
@@ -612,9 +621,9 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   auto step = [&](auto u_c, int j) __attribute__((always_inline)) {
     constexpr int U = decltype(u_c)::value;
     constexpr int par = U & 1;
-    using slot_c = ic<(U + kPStages - 2) % kPStages>;
+    using slot_c = ic<(U + kPDist) % kPStages>;
     if (j > nst) return;  // uniform over the CTA: past the last stage
-    step_sync();
+    if constexpr (U % kPSync == 0) step_sync();
     if (__builtin_expect(j <= W && W > 0, 1)) {
       group_setup(slot_c{});
       if (__builtin_expect(j >= j_diag, 0)) mask_scores(sc[par], j, j == W);
@@ -630,7 +639,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   // loads its groups.
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) pb[1][qs][0] = pb[1][qs][1] = u32x4{};
-  step_sync();
+  sync_groups(ic<kPDist - 2>{});  // stage 0 landed
   group_now(ic<-1>{});
   if (W > 0) {
     qk_plain(sc[0], 0);
