@@ -7,7 +7,8 @@
 //
 // One CTA per (request, 256 query rows, head); 8 waves x 32 query rows, two waves per SIMD (the
 // kernel is a template on QS, the 32-row query sub-blocks per wave; QS = 2, 4 waves x 64 rows with
-// one wave per SIMD, measures the same and is kept buildable).
+// one wave per SIMD, measured the same with a barrier per step and is kept buildable; with the
+// current ring it spills and runs ~12 % slower).
 //  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 6-stage
 //    LDS ring filled by 16-byte DMA loads: waves 0-3 load the K tile, waves 4-7 the V tile (one
 //    wave of each per SIMD). K rows (384 B) are stored with the
