@@ -545,6 +545,7 @@ static int prefill_launch(const char* who, const void* q, int64_t q_stride_t, in
   p.out = static_cast<__bf16*>(out);
   p.out_stride_t = out_stride_t;
   p.out_stride_h = out_stride_h;
+  p.out_16b = aligned(out, 16) && out_stride_t % 8 == 0 && out_stride_h % 8 == 0;
   p.lse = lse;
   p.lse_stride_t = lse_stride_t;
   return hip_status(mla::launch_prefill(p, total_q, (hipStream_t)stream), who);

@@ -95,6 +95,7 @@ struct PrefillParams {
   float scale_log2;
   __bf16* out;  // [T, H, 128]
   int64_t out_stride_t, out_stride_h;
+  int32_t out_16b;  // out rows start 16-byte aligned (base and strides): 16-byte stores
   float* lse;  // [T, H] or null
   int64_t lse_stride_t;
 };

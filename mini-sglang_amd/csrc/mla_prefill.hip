@@ -47,6 +47,8 @@ constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
 constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
 constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
 constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
+constexpr int kPHeads = 2;  // heads per CTA, one after the other (their request metadata and
+                            // page-table sources are read once)
 // Steps between CTA barriers (1 or 2). Step j loads stage j + kPDist; a barrier step makes
 // stages up to j + kPSync visible to every wave, and the ring has kPSync - 1 more stages than one
 // barrier per step needs, so that a wave one step ahead of another never refills a stage the other
@@ -178,21 +180,26 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = p.heads;
 
-  // ---- work item: request b, query block qb, head h (heads fastest); the last items (the
-  // latest query blocks, which see the most keys) are dispatched first
+  // ---- work item: request b, query block qb, head group hg of kPHeads heads (groups fastest),
+  // whose heads the CTA runs one after the other on the same request metadata and page-table
+  // sources; the last items (the latest query blocks, which see the most keys) are dispatched first
+  const int HG = (H + kPHeads - 1) / kPHeads;
   auto items_of = [&](int r) __attribute__((always_inline)) {
-    return r < p.batch ? ((p.cu_seqlens_q[r + 1] - p.cu_seqlens_q[r] + kPrefillRows - 1) / kPrefillRows) * H : 0;
+    return r < p.batch ? ((p.cu_seqlens_q[r + 1] - p.cu_seqlens_q[r] + kPrefillRows - 1) / kPrefillRows) * HG : 0;
   };
   int total = 0;
   for (int c0 = 0; c0 < p.batch; c0 += 64) total += wave_sum(items_of(c0 + lane));
   total = __builtin_amdgcn_readfirstlane(total);
   const int item = total - 1 - (int)blockIdx.x;
-  int b = -1, local = 0;
+  int b = -1, local = 0, q0 = 0, E = 0, L = 0;
   if (item >= 0) {
     int acc = 0;
     for (int c0 = 0; c0 < p.batch && b < 0; c0 += 64) {
       const int r = c0 + lane;
-      const int n = items_of(r);
+      const bool in = r < p.batch;
+      // the request's query range and key count come with the scan (no second memory round trip)
+      const int lo = in ? p.cu_seqlens_q[r] : 0, hi = in ? p.cu_seqlens_q[r + 1] : 0, lk = in ? p.seq_lens_k[r] : 0;
+      const int n = in ? ((hi - lo + kPrefillRows - 1) / kPrefillRows) * HG : 0;
       int incl = n;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -205,6 +212,9 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
         const int fl = __builtin_ctzll(hit);
         b = c0 + fl;
         local = item - acc - __shfl(excl, fl);
+        q0 = __shfl(lo, fl);
+        E = __shfl(hi, fl) - q0;
+        L = __shfl(lk, fl);
       }
       acc += __shfl(incl, 63);
     }
@@ -212,11 +222,11 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   b = __builtin_amdgcn_readfirstlane(b);
   if (b < 0) return;  // uniform: beyond the last item
   local = __builtin_amdgcn_readfirstlane(local);
-  const int h = local % H;
-  const int qb = local / H;
-  const int q0 = p.cu_seqlens_q[b];
-  const int E = p.cu_seqlens_q[b + 1] - q0;
-  const int L = p.seq_lens_k[b];
+  q0 = __builtin_amdgcn_readfirstlane(q0);
+  E = __builtin_amdgcn_readfirstlane(E);
+  L = __builtin_amdgcn_readfirstlane(L);
+  const int hg = local % HG;
+  const int qb = local / HG;
   const int P = L - E;  // prefix length
   const int row0 = qb * kPrefillRows + wave * kPRowsPerWave;  // this wave's first query row in the request
   const int cta_rows_end = min(E, (qb + 1) * kPrefillRows);
@@ -230,6 +240,12 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int c32 = lane & 31;
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
+
+#pragma nounroll
+  for (int hi = 0; hi < kPHeads; ++hi) {
+  const int h = kPHeads * hg + hi;
+  if (h >= H) break;  // uniform
+  if (hi > 0) barrier_lds();  // every wave is done with the previous head's ring and sources
   // a K row is 128 nope dims at kbase (+ token row) and 64 rope dims rope_delta bytes after them
   // (the host checks 0 <= rope_delta < 2^31 for every head)
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
@@ -264,13 +280,21 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const bool staged = nst <= kPMaxGroups;
   const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
   for (int g = threadIdx.x; g <= n_defer; g += kPWaves * 64) {
+    if (hi > 0) {  // the previous head's sources, moved by one head
+      MLA_LDS u32x4* e = reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g);
+      const u32x4 v = *e;
+      const uint64_t ka = ((uint64_t)v[1] << 32 | v[0]) + (uint64_t)(p.k_head_stride * 2);
+      const uint64_t va = ((uint64_t)v[3] << 32 | v[2]) + (uint64_t)(p.v_head_stride * 2);
+      *e = u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
+      continue;
+    }
     const int t0 = g < n_defer ? g * kPStage : 0;
     const uint32_t pid = (uint32_t)min(max(p.page_table[(int64_t)b * p.pt_stride + (t0 >> p.log2_ps)], 0), p.num_pages - 1);
     const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
     const uint64_t va = (uint64_t)stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
     *reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g) = u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
   }
-  __syncthreads();
+  barrier_lds();  // the source table is written (the queries may still be in flight)
 
   // ---- DMA of stage n (32 tokens of one page: page_size >= 64); rows past the last key load the
   // last key. LDS position s (16 bytes each) of the K tile holds token s / 24, chunk kswz(s % 24);
@@ -407,10 +431,12 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   };
   // a barrier step n: stages n + 1 .. n + kPSync landed (kPDist - 1 - kPSync groups follow them)
   auto step_sync = [&]() __attribute__((always_inline)) { sync_groups(ic<kPDist - 1 - kPSync>{}); };
+
+  for (int g = 0; g < kPDist - 1; ++g) group_now(ic<-1>{});
   // the queries stay in registers for the whole kernel (with QS = 2 in the accumulation registers,
-  // which the score MFMAs read) and have landed here, before the first loads of the ring: the DMA
-  // loads are inline assembly the compiler does not count, so a wait for the queries later on
-  // would be a full vmcnt(0)
+  // which the score MFMAs read) and have landed here, with the first loads of the ring issued
+  // behind them: the DMA loads are inline assembly the compiler does not count, so its wait for
+  // the queries is a full vmcnt(0), which belongs here and not inside the steps
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
@@ -418,8 +444,6 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
       if constexpr (QS == 2) asm volatile("" : "=a"(qf[qs][ks]) : "0"(qf[qs][ks]));
       else asm volatile("" : "+v"(qf[qs][ks]));
     }
-
-  for (int g = 0; g < kPDist - 1; ++g) group_now(ic<-1>{});
 
   // ---- per-lane LDS read offsets
   // K operand of k-step ks = 4m + r: chunk 8m + 2r + g32 of key c32 at k_off[r] + 128m
@@ -658,20 +682,37 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
     const float l_tot = sum_halves(l_run[qs]);
     if (row >= E || wave_rows == 0) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    __bf16* orow = p.out + (int64_t)(q0 + row) * p.out_stride_t + (int64_t)h * p.out_stride_h + 4 * g32;
+    __bf16* orow = p.out + (int64_t)(q0 + row) * p.out_stride_t + (int64_t)h * p.out_stride_h;
+    auto packed = [&](int db, int i4) {  // dims 32db + 8i4 + 4g32 .. +4 of this lane's row
+      u32x2 v;
+      v[0] = pack_bf16x2(O[db][qs][4 * i4 + 0] * inv, O[db][qs][4 * i4 + 1] * inv);
+      v[1] = pack_bf16x2(O[db][qs][4 * i4 + 2] * inv, O[db][qs][4 * i4 + 3] * inv);
+      return v;
+    };
+    if (p.out_16b) {
+      // 16-byte stores (half the store instructions): the lanes of a row (c32, g32 = 0, 1) swap
+      // one 8-byte part of each 16 dims, so that lane g32 holds dims 32db + 16m + 8g32 .. +8
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 v;
-        v[0] = pack_bf16x2(O[db][qs][4 * i4 + 0] * inv, O[db][qs][4 * i4 + 1] * inv);
-        v[1] = pack_bf16x2(O[db][qs][4 * i4 + 2] * inv, O[db][qs][4 * i4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * i4) = v;
-      }
+        for (int m = 0; m < 2; ++m) {
+          const u32x2 va = packed(db, 2 * m), vb = packed(db, 2 * m + 1);
+          const u32x2 x = g32 == 0 ? vb : va;
+          const uint32_t y0 = (uint32_t)__shfl_xor((int)x[0], 32), y1 = (uint32_t)__shfl_xor((int)x[1], 32);
+          const u32x4 v = g32 == 0 ? u32x4{va[0], va[1], y0, y1} : u32x4{y0, y1, vb[0], vb[1]};
+          *reinterpret_cast<u32x4*>(orow + 32 * db + 16 * m + 8 * g32) = v;
+        }
+    } else {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * i4 + 4 * g32) = packed(db, i4);
+    }
     if (p.lse != nullptr && g32 == 0)
       p.lse[(int64_t)(q0 + row) * p.lse_stride_t + h] =
           l_tot > 0.f ? (m_ref[qs] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
   }
+  }  // heads of the group
 }
 
 }  // namespace
@@ -681,7 +722,7 @@ constexpr int kPrefillQS = 1;
 
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream) {
   // upper bound on sum_b ceil(E_b / 256) over the batch, times the heads
-  const int64_t items = ((int64_t)(total_q + kPrefillRows - 1) / kPrefillRows + p.batch) * p.heads;
+  const int64_t items = ((int64_t)(total_q + kPrefillRows - 1) / kPrefillRows + p.batch) * ((p.heads + kPHeads - 1) / kPHeads);
   if (items <= 0) return hipSuccess;
   hipLaunchKernelGGL(mla_prefill_kernel<kPrefillQS>, dim3((unsigned)items), dim3(8 / kPrefillQS * 64), 0, stream, p);
   return hipGetLastError();
