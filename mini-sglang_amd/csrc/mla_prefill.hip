@@ -241,6 +241,20 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
 
+  // queries of head h: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the
+  // extend); a head's are loaded before the previous head's output is written
+  bf16x8 qf[QS][12];
+  auto load_q = [&](int hq) __attribute__((always_inline)) {
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      const int row = row0 + 32 * qs + c32;
+      const bool ok = row < E;
+      const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)hq * p.q_stride_h + 8 * g32;
+#pragma unroll
+      for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = ok ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ks) : bf16x8{};
+    }
+  };
+
 #pragma nounroll
   for (int hi = 0; hi < kPHeads; ++hi) {
   const int h = kPHeads * hg + hi;
@@ -264,17 +278,9 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
     return base + ((uint64_t)pid * page_bytes + (uint32_t)((t0 & ps_mask) * row_bytes));
   };
 
-  // ---- queries, loaded first so that their latency overlaps the page-table reads below:
-  // qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the extend)
-  bf16x8 qf[QS][12];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    const int row = row0 + 32 * qs + c32;
-    const bool ok = row < E;
-    const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)h * p.q_stride_h + 8 * g32;
-#pragma unroll
-    for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = ok ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ks) : bf16x8{};
-  }
+  // ---- the first head's queries, loaded first so that their latency overlaps the page-table
+  // reads below
+  if (hi == 0) load_q(h);
   // ---- source addresses of the CTA's full stages (s_src[n_defer]: the first stage's, the source
   // of dummy groups); a CTA with more stages than that computes each stage's source when it loads it
   const bool staged = nst <= kPMaxGroups;
@@ -433,10 +439,12 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   auto step_sync = [&]() __attribute__((always_inline)) { sync_groups(ic<kPDist - 1 - kPSync>{}); };
 
   for (int g = 0; g < kPDist - 1; ++g) group_now(ic<-1>{});
-  // the queries stay in registers for the whole kernel (with QS = 2 in the accumulation registers,
+  // the queries stay in registers for the whole head (with QS = 2 in the accumulation registers,
   // which the score MFMAs read) and have landed here, with the first loads of the ring issued
-  // behind them: the DMA loads are inline assembly the compiler does not count, so its wait for
-  // the queries is a full vmcnt(0), which belongs here and not inside the steps
+  // behind them. The wait is explicit and full: the compiler counts neither the DMA loads (inline
+  // assembly) nor their place behind the previous head's output stores, which were issued after
+  // this head's queries, so a count of its own could let a query load still be in flight.
+  wait_vmcnt<0>();
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
@@ -674,6 +682,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   for (int j0 = 0; j0 <= nst; j0 += kPUnroll)
     static_for<kPUnroll>([&](auto u_c) __attribute__((always_inline)) { step(u_c, j0 + decltype(u_c)::value); });
   wait_vmcnt<0>();  // the last groups' loads into LDS have landed before the CTA ends
+  if (hi + 1 < kPHeads && h + 1 < H) load_q(h + 1);  // the registers are free: the steps are done
 
   // ---- finalise: lane holds query column c32 and dims 32db + 8(i/4) + 4*g32 + i%4
 #pragma unroll
