@@ -241,8 +241,10 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int ps_mask = (1 << p.log2_ps) - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(MLA_LDS char*)smem;
 
-  // queries of head h: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (zeros past the
-  // extend); a head's are loaded before the previous head's output is written
+  // queries of head h: qf[qs][ks] = row row0 + 32qs + c32, dims 16ks + 8g32 .. +8 (a column past the
+  // extend loads the first row: finite scores in a column whose output is not written; no select,
+  // so that nothing waits for these loads before the first ring loads are issued); a head's are
+  // loaded before the previous head's output is written
   bf16x8 qf[QS][12];
   auto load_q = [&](int hq) __attribute__((always_inline)) {
 #pragma unroll
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
       const bool ok = row < E;
       const __bf16* qrow = p.q + (int64_t)(q0 + (ok ? row : 0)) * p.q_stride_t + (int64_t)hq * p.q_stride_h + 8 * g32;
 #pragma unroll
-      for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = ok ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ks) : bf16x8{};
+      for (int ks = 0; ks < 12; ++ks) qf[qs][ks] = *reinterpret_cast<const bf16x8*>(qrow + 16 * ks);
     }
   };
 
@@ -278,27 +280,43 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
     return base + ((uint64_t)pid * page_bytes + (uint32_t)((t0 & ps_mask) * row_bytes));
   };
 
-  // ---- the first head's queries, loaded first so that their latency overlaps the page-table
-  // reads below
-  if (hi == 0) load_q(h);
   // ---- source addresses of the CTA's full stages (s_src[n_defer]: the first stage's, the source
   // of dummy groups); a CTA with more stages than that computes each stage's source when it loads it
   const bool staged = nst <= kPMaxGroups;
   const int n_defer = staged ? min(nst, L >> 5) : 0;  // stages the pipelined step may load itself
-  for (int g = threadIdx.x; g <= n_defer; g += kPWaves * 64) {
-    if (hi > 0) {  // the previous head's sources, moved by one head
+  if (hi == 0) {
+    // the page-table reads, then the first head's queries, then the table writes: the writes wait
+    // for the page-table reads alone, and the queries stay in flight behind the first ring loads
+    constexpr int kPer = (kPMaxGroups + kPWaves * 64) / (kPWaves * 64);  // entries per thread
+    int pid_u[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int g = threadIdx.x + kPWaves * 64 * u;
+      const int t0 = g < n_defer ? g * kPStage : 0;  // (an unconditional read: the first page's entry)
+      pid_u[u] = p.page_table[(int64_t)b * p.pt_stride + (t0 >> p.log2_ps)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(h);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int g = threadIdx.x + kPWaves * 64 * u;
+      if (g > n_defer) continue;
+      const int t0 = g < n_defer ? g * kPStage : 0;
+      const uint32_t pid = (uint32_t)min(max(pid_u[u], 0), p.num_pages - 1);
+      const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
+      const uint64_t va = (uint64_t)stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
+      *reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g) =
+          u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
+    }
+  } else {
+    for (int g = threadIdx.x; g <= n_defer; g += kPWaves * 64) {  // the previous head's, moved by a head
       MLA_LDS u32x4* e = reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g);
       const u32x4 v = *e;
       const uint64_t ka = ((uint64_t)v[1] << 32 | v[0]) + (uint64_t)(p.k_head_stride * 2);
       const uint64_t va = ((uint64_t)v[3] << 32 | v[2]) + (uint64_t)(p.v_head_stride * 2);
       *e = u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
-      continue;
     }
-    const int t0 = g < n_defer ? g * kPStage : 0;
-    const uint32_t pid = (uint32_t)min(max(p.page_table[(int64_t)b * p.pt_stride + (t0 >> p.log2_ps)], 0), p.num_pages - 1);
-    const uint64_t ka = (uint64_t)stage_src(kbase, pid, t0, kpage_bytes, krow_bytes);
-    const uint64_t va = (uint64_t)stage_src(vbase, pid, t0, vpage_bytes, vrow_bytes);
-    *reinterpret_cast<MLA_LDS u32x4*>((MLA_LDS char*)s_src + 16 * g) = u32x4{(uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32)};
   }
   barrier_lds();  // the source table is written (the queries may still be in flight)
 
