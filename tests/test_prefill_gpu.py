@@ -47,10 +47,30 @@ def test_prefill_ragged(ps):
     check_case(case)
 
 
-@pytest.mark.parametrize("heads", [1, 16, 64])
+@pytest.mark.parametrize("heads", [1, 3, 5, 16, 64])
 def test_prefill_heads(heads):
+    """A CTA runs a pair of heads one after the other; odd counts leave the last pair one head."""
     case = make_prefill_case(heads, 64, extends=[129, 64], prefixes=[200, 0], seed=heads)
     check_case(case)
+
+
+def test_prefill_output_rows_8_byte_aligned():
+    """An output whose head stride is a multiple of 4 but not 8 elements takes the 8-byte stores:
+    the same bits as a contiguous output, and the columns past 128 untouched."""
+    case = make_prefill_case(5, 64, extends=[300, 45], prefixes=[77, 640], seed=11)
+    T, H, _ = case.q.shape
+    out_c, lse_c = run_prefill(case)
+    buf = torch.full((T, H, 132), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out = buf[..., :128]
+    lse = torch.full((T, H), float("nan"), dtype=torch.float32, device=DEV)
+    lib.mla_prefill(
+        case.q.to(DEV), case.k_pool.to(DEV), case.v_pool.to(DEV), case.page_table.to(DEV),
+        case.cu_seqlens_q.to(DEV), case.seq_lens_k.to(DEV), R.DEFAULT_SCALE, out, lse,
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(out.float().cpu(), out_c)
+    assert torch.equal(lse.cpu(), lse_c)
+    assert torch.isnan(buf[..., 128:].float()).all()
 
 
 def test_prefill_no_prefix_is_causal_sdpa():
