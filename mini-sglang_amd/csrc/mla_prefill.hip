@@ -47,8 +47,6 @@ constexpr int kPVRowBytes = kPrefillVDim * 2;           // 256
 constexpr int kPKBytes = kPStage * kPKRowBytes;         // 12288
 constexpr int kPVBytes = kPStage * kPVRowBytes;         // 8192
 constexpr int kPStageBytes = kPKBytes + kPVBytes;       // 20480
-constexpr int kPHeads = 2;  // heads per CTA, one after the other (their request metadata and
-                            // page-table sources are read once)
 // Steps between CTA barriers (1 or 2). Step j loads stage j + kPDist; a barrier step makes
 // stages up to j + kPSync visible to every wave, and the ring has kPSync - 1 more stages than one
 // barrier per step needs, so that a wave one step ahead of another never refills a stage the other
@@ -180,10 +178,11 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = p.heads;
 
-  // ---- work item: request b, query block qb, head group hg of kPHeads heads (groups fastest),
+  // ---- work item: request b, query block qb, head group hg of p.heads_per_cta heads (groups fastest),
   // whose heads the CTA runs one after the other on the same request metadata and page-table
   // sources; the last items (the latest query blocks, which see the most keys) are dispatched first
-  const int HG = (H + kPHeads - 1) / kPHeads;
+  const int HPC = p.heads_per_cta;
+  const int HG = (H + HPC - 1) / HPC;
   auto items_of = [&](int r) __attribute__((always_inline)) {
     return r < p.batch ? ((p.cu_seqlens_q[r + 1] - p.cu_seqlens_q[r] + kPrefillRows - 1) / kPrefillRows) * HG : 0;
   };
@@ -258,8 +257,8 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   };
 
 #pragma nounroll
-  for (int hi = 0; hi < kPHeads; ++hi) {
-  const int h = kPHeads * hg + hi;
+  for (int hi = 0; hi < HPC; ++hi) {
+  const int h = HPC * hg + hi;
   if (h >= H) break;  // uniform
   if (hi > 0) barrier_lds();  // every wave is done with the previous head's ring and sources
   // a K row is 128 nope dims at kbase (+ token row) and 64 rope dims rope_delta bytes after them
@@ -700,7 +699,7 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   for (int j0 = 0; j0 <= nst; j0 += kPUnroll)
     static_for<kPUnroll>([&](auto u_c) __attribute__((always_inline)) { step(u_c, j0 + decltype(u_c)::value); });
   wait_vmcnt<0>();  // the last groups' loads into LDS have landed before the CTA ends
-  if (hi + 1 < kPHeads && h + 1 < H) load_q(h + 1);  // the registers are free: the steps are done
+  if (hi + 1 < HPC && h + 1 < H) load_q(h + 1);  // the registers are free: the steps are done
 
   // ---- finalise: lane holds query column c32 and dims 32db + 8(i/4) + 4*g32 + i%4
 #pragma unroll
@@ -747,10 +746,26 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
 // query sub-blocks of 32 rows per wave: 1 (8 waves, two per SIMD) or 2 (4 waves, one per SIMD)
 constexpr int kPrefillQS = 1;
 
-hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream) {
-  // upper bound on sum_b ceil(E_b / 256) over the batch, times the heads
-  const int64_t items = ((int64_t)(total_q + kPrefillRows - 1) / kPrefillRows + p.batch) * ((p.heads + kPHeads - 1) / kPHeads);
-  if (items <= 0) return hipSuccess;
+hipError_t launch_prefill(const PrefillParams& p0, int32_t total_q, hipStream_t stream) {
+  // upper bound on sum_b ceil(E_b / 256) over the batch
+  const int64_t blocks = (int64_t)(total_q + kPrefillRows - 1) / kPrefillRows + p0.batch;
+  if (blocks <= 0 || p0.heads <= 0) return hipSuccess;
+  // Two heads per CTA (the second head's request metadata and page-table sources come for free,
+  // its queries are loaded during the first head's output) when the one-head CTAs would fill the
+  // compute units at least eight times over; a smaller batch keeps one head per CTA, whose finer
+  // grain the hardware's CTA scheduling balances better (a 64-head prefill of one 256-row block
+  // takes twice as long with two heads per CTA).
+  static int cus_of[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  int cus = dev >= 0 && dev < 64 ? cus_of[dev] : 0;
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev >= 0 && dev < 64) cus_of[dev] = cus;
+  }
+  PrefillParams p = p0;
+  p.heads_per_cta = blocks * p.heads >= 8LL * cus ? 2 : 1;
+  const int64_t items = blocks * ((p.heads + p.heads_per_cta - 1) / p.heads_per_cta);
   hipLaunchKernelGGL(mla_prefill_kernel<kPrefillQS>, dim3((unsigned)items), dim3(8 / kPrefillQS * 64), 0, stream, p);
   return hipGetLastError();
 }

@@ -49,7 +49,7 @@ def test_prefill_ragged(ps):
 
 @pytest.mark.parametrize("heads", [1, 3, 5, 16, 64])
 def test_prefill_heads(heads):
-    """A CTA runs a pair of heads one after the other; odd counts leave the last pair one head."""
+    """Head counts 1..64, odd ones included (one head per CTA at these sizes)."""
     case = make_prefill_case(heads, 64, extends=[129, 64], prefixes=[200, 0], seed=heads)
     check_case(case)
 
@@ -222,3 +222,30 @@ def test_prefill_full_bench_batch_sampled_rows_and_chunking():
         o_ref, lse_ref = R._attend(qs, k, v, R.DEFAULT_SCALE, mask[None])
         torch.testing.assert_close(out[b * E + pick.to(DEV)].float().cpu(), o_ref.transpose(0, 1), **O_TOL)
         torch.testing.assert_close(lse[b * E + pick.to(DEV)].cpu(), lse_ref.transpose(0, 1), **LSE_TOL)
+
+
+def test_prefill_head_pairs_odd_heads_chunk_invariant():
+    """A batch large enough for two heads per CTA (one 8192-row extend: 33 row blocks x 63 heads
+    is at least 8 CTAs per compute unit) with an odd head count, so the last CTA of each block
+    runs one head: bit for bit the same as the same rows prefilled as 1024-row chunks, which are
+    small enough to run one head per CTA."""
+    H, E, P, ps = 63, 8192, 300, 64
+    print(f"[prefill head pairs] H={H} E={E} P={P}", flush=True)
+    case = make_prefill_case(H, ps, extends=[E], prefixes=[P], device=DEV, seed=5)
+
+    def run(q, cu, lens):
+        out = torch.full((q.shape[0], H, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+        lse = torch.full((q.shape[0], H), float("nan"), dtype=torch.float32, device=DEV)
+        lib.mla_prefill(q, case.k_pool, case.v_pool, case.page_table, cu, lens, R.DEFAULT_SCALE, out, lse)
+        torch.cuda.synchronize()
+        return out, lse
+
+    out, lse = run(case.q, case.cu_seqlens_q, case.seq_lens_k)
+    assert not torch.isnan(lse).any()
+    C = 1024
+    cu = torch.tensor([0, C], dtype=torch.int32, device=DEV)
+    for c in range(E // C):
+        lens = torch.tensor([P + C * (c + 1)], dtype=torch.int32, device=DEV)
+        o, l = run(case.q[C * c: C * (c + 1)].contiguous(), cu, lens)
+        assert torch.equal(o.view(torch.int16), out[C * c: C * (c + 1)].view(torch.int16)), c
+        assert torch.equal(l, lse[C * c: C * (c + 1)]), c
