@@ -96,7 +96,6 @@ struct PrefillParams {
   __bf16* out;  // [T, H, 128]
   int64_t out_stride_t, out_stride_h;
   int32_t out_16b;  // out rows start 16-byte aligned (base and strides): 16-byte stores
-  int32_t heads_per_cta;  // 1 or 2 heads per CTA, one after the other (set by launch_prefill)
   float* lse;  // [T, H] or null
   int64_t lse_stride_t;
 };

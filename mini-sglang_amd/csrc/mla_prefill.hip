@@ -166,7 +166,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int QS>
+template <int QS, int HPC>  // HPC: heads per CTA, run one after the other
 __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const PrefillParams p) {
   constexpr int kPWaves = 8 / QS;
   constexpr int kPRowsPerWave = 32 * QS;
@@ -178,10 +178,9 @@ __global__ __launch_bounds__(8 / QS * 64, 1) void mla_prefill_kernel(const Prefi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = p.heads;
 
-  // ---- work item: request b, query block qb, head group hg of p.heads_per_cta heads (groups fastest),
+  // ---- work item: request b, query block qb, head group hg of HPC heads (groups fastest),
   // whose heads the CTA runs one after the other on the same request metadata and page-table
   // sources; the last items (the latest query blocks, which see the most keys) are dispatched first
-  const int HPC = p.heads_per_cta;
   const int HG = (H + HPC - 1) / HPC;
   auto items_of = [&](int r) __attribute__((always_inline)) {
     return r < p.batch ? ((p.cu_seqlens_q[r + 1] - p.cu_seqlens_q[r] + kPrefillRows - 1) / kPrefillRows) * HG : 0;
@@ -763,10 +762,12 @@ hipError_t launch_prefill(const PrefillParams& p0, int32_t total_q, hipStream_t 
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
-  PrefillParams p = p0;
-  p.heads_per_cta = blocks * p.heads >= 8LL * cus ? 2 : 1;
-  const int64_t items = blocks * ((p.heads + p.heads_per_cta - 1) / p.heads_per_cta);
-  hipLaunchKernelGGL(mla_prefill_kernel<kPrefillQS>, dim3((unsigned)items), dim3(8 / kPrefillQS * 64), 0, stream, p);
+  if (blocks * p0.heads >= 8LL * cus)
+    hipLaunchKernelGGL((mla_prefill_kernel<kPrefillQS, 2>), dim3((unsigned)(blocks * ((p0.heads + 1) / 2))),
+                       dim3(8 / kPrefillQS * 64), 0, stream, p0);
+  else
+    hipLaunchKernelGGL((mla_prefill_kernel<kPrefillQS, 1>), dim3((unsigned)(blocks * p0.heads)),
+                       dim3(8 / kPrefillQS * 64), 0, stream, p0);
   return hipGetLastError();
 }
 
