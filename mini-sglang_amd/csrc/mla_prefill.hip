@@ -5,13 +5,17 @@
 // [.., H, 192] has them adjacent; the latent-decompression scratch keeps one rope copy per token,
 // shared by all heads, after the heads' [k_nope | v] blocks).
 //
-// One CTA per (request, 256 query rows, head); 8 waves x 32 query rows, two waves per SIMD (the
-// kernel is a template on QS, the 32-row query sub-blocks per wave; QS = 2, 4 waves x 64 rows with
-// one wave per SIMD, measured the same with a barrier per step and is kept buildable; with the
-// current ring it spills and runs ~12 % slower).
-//  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 6-stage
+// One CTA per (request, 256 query rows, group of HPC = 1 or 2 heads), the heads of a group run one
+// after the other (the launcher takes two when one-head CTAs would fill the GPU eight times over:
+// the second head reuses the request lookup and the page-table sources, and its queries load
+// during the first head's output); 8 waves x 32 query rows, two waves per SIMD (the kernel is a
+// template on QS, the 32-row query sub-blocks per wave; QS = 2, 4 waves x 64 rows with one wave
+// per SIMD, measured the same with a barrier per step and is kept buildable; with the current ring
+// it spills and runs ~12 % slower).
+//  * Keys stream in stages of 32 tokens (K 12 KB + V 8 KB) through a 7-stage
 //    LDS ring filled by 16-byte DMA loads: waves 0-3 load the K tile, waves 4-7 the V tile (one
-//    wave of each per SIMD). K rows (384 B) are stored with the
+//    wave of each per SIMD); loads run four stages ahead and the CTA synchronises once per two
+//    steps. K rows (384 B) are stored with the
 //    16-byte chunk index XOR ((token >> 1) & 7) inside each 8-chunk group, V rows
 //    (256 B) with XOR 4 * (token & 3): the K operand reads (ds_read_b128) and the
 //    transposing V reads (ds_read_b64_tr_b16) are then bank-conflict free, as
@@ -19,18 +23,19 @@
 //    XOR 2 * (token & 3) leave both 2-way conflicted).
 //  * S^T[32 keys x 32 queries] = K . Q^T and O^T[128 dims x 32 queries] +=
 //    V^T . P^T on 32x32x16 bf16 MFMA; queries (the B operand) and O stay in
-//    registers for the whole kernel (216 VGPRs with QS = 1).
+//    registers for the whole head.
 //  * Software pipeline over the stages: step j issues the value MFMAs of stage
 //    j-1 and the score MFMAs of stage j+1 while the vector ALU runs the online
 //    softmax of stage j, the two instruction streams interleaved slot by slot
-//    (one MFMA per slot). Steps that need masking (the diagonal), and the
-//    first and last steps of a wave, run the three parts one after another.
+//    (one MFMA per slot). Every step of a wave runs this same body: a diagonal
+//    step first masks its stage's scores, the first step sets the reference,
+//    and the last step's score pass works on a fully masked stage.
 //  * Online softmax in the log2 domain against a lazy row reference: the exact
 //    max of the wave's first stage, moved (with O and l rescaled, and the
 //    stage redone) only when a stage's numerators sum past 2^32.
-//  * The heads of one (request, query block) are consecutive CTAs, so the
-//    query blocks of one head are 'heads' CTAs apart and, with heads a
-//    multiple of 8, land on the same XCD and share its L2 for K/V.
+//  * The head groups of one (request, query block) are consecutive CTAs, so the
+//    query blocks of one group are H / HPC CTAs apart and, with that a multiple
+//    of 8, land on the same XCD and share its L2 for K/V.
 #include <type_traits>
 
 #include "mla_common.h"
