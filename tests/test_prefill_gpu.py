@@ -249,3 +249,29 @@ def test_prefill_head_pairs_odd_heads_chunk_invariant():
         o, l = run(case.q[C * c: C * (c + 1)].contiguous(), cu, lens)
         assert torch.equal(o.view(torch.int16), out[C * c: C * (c + 1)].view(torch.int16)), c
         assert torch.equal(l, lse[C * c: C * (c + 1)]), c
+
+
+def test_prefill_head_pairs_unstaged_long_prefix_chunk_invariant():
+    """Two heads per CTA over more stages than the kernel stages sources for (a 30,000-token
+    prefix: the later query blocks read their page ids per stage, so the second head's sources
+    are computed, not moved): bit for bit the same as 1024-row chunks (one head per CTA)."""
+    H, E, P, ps = 64, 8192, 30000, 64
+    print(f"[prefill head pairs, long prefix] H={H} E={E} P={P}", flush=True)
+    case = make_prefill_case(H, ps, extends=[E], prefixes=[P], device=DEV, seed=6)
+
+    def run(q, cu, lens):
+        out = torch.full((q.shape[0], H, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+        lse = torch.full((q.shape[0], H), float("nan"), dtype=torch.float32, device=DEV)
+        lib.mla_prefill(q, case.k_pool, case.v_pool, case.page_table, cu, lens, R.DEFAULT_SCALE, out, lse)
+        torch.cuda.synchronize()
+        return out, lse
+
+    out, lse = run(case.q, case.cu_seqlens_q, case.seq_lens_k)
+    assert not torch.isnan(lse).any()
+    C = 1024
+    cu = torch.tensor([0, C], dtype=torch.int32, device=DEV)
+    for c in range(E // C):
+        lens = torch.tensor([P + C * (c + 1)], dtype=torch.int32, device=DEV)
+        o, l = run(case.q[C * c: C * (c + 1)].contiguous(), cu, lens)
+        assert torch.equal(o.view(torch.int16), out[C * c: C * (c + 1)].view(torch.int16)), c
+        assert torch.equal(l, lse[C * c: C * (c + 1)]), c
