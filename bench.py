@@ -167,8 +167,7 @@ def bench_decode(args):
     ctas = lib.device_cu_count(0)
     plan_np, slots = lib.decode_plan(case.lens, case.page_size, ctas)
     plan = torch.from_numpy(plan_np).to(dev)
-    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=dev)
-    ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=dev)
+    ws_o, ws_lse = lib.decode_workspace(slots, H, dev)
     out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
     lse = torch.empty((B, H), dtype=torch.float32, device=dev)
     req_info = plan[ctas * lib.PLAN_CTA_INTS :]
@@ -403,8 +402,7 @@ class _DecodeCall:
         self.ctas = lib.device_cu_count(0)
         plan_np, self.slots = lib.decode_plan(case.lens, case.page_size, self.ctas)
         self.plan = torch.from_numpy(plan_np).to(dev)
-        self.ws_o = torch.empty((max(self.slots, 1), H, 512), dtype=torch.float32, device=dev)
-        self.ws_lse = torch.empty((max(self.slots, 1), H), dtype=torch.float32, device=dev)
+        self.ws_o, self.ws_lse = lib.decode_workspace(self.slots, H, dev)
         self.out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
         self.lse = torch.empty((B, H), dtype=torch.float32, device=dev)
 

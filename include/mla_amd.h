@@ -46,6 +46,14 @@ enum {
 #define MLA_PLAN_MAX_CTA_BLOCKS 512
 #define MLA_PLAN_MAX_CTA_REQUESTS 128
 
+/*
+ * Split-KV partial outputs (the decode workspace ws_o): one row of 512 bf16 per (slot, head), the
+ * piece's normalised output, in chunk order: 16-byte chunk c (elements 8c .. 8c+7) holds value dims
+ * 32 (c / 4) + 4 (c % 4) + {0, 1, 2, 3} and then 32 (c / 4) + 16 + 4 (c % 4) + {0, 1, 2, 3}. This is
+ * the order the decode kernels' registers hold them in (one 16-byte store per chunk); only the
+ * library's merge reads these rows. Their LSEs (ws_lse) are fp32 natural logs.
+ */
+
 /* Message for the last failed call on this thread ("" if none). */
 const char *mla_last_error(void);
 
@@ -137,7 +145,7 @@ int mla_decode_plan(const int32_t *seq_lens, int32_t batch, int32_t page_size,
  *   page_table [batch, >= ceil(seq_len/page_size)] int32, row stride pt_stride
  *   seq_lens [batch] int32 (device_len, includes the token being decoded)
  *   plan     device copy of mla_decode_plan's cta_ranges followed by req_info
- *   ws_o     [ws_slots, heads, 512] fp32 (normalised partial outputs),
+ *   ws_o     [ws_slots, heads, 512] bf16 (normalised partial outputs, chunk order above),
  *            ws_lse [ws_slots, heads] fp32
  *   out      [batch, heads, 512] strides (out_stride_b, out_stride_h)
  *   lse      [batch, heads] fp32 (row stride lse_stride_b) or NULL
@@ -152,14 +160,14 @@ int mla_decode_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h, const
                     int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
                     const int32_t *page_table, int64_t pt_stride, const int32_t *seq_lens,
                     int32_t batch, int32_t heads, float scale, const int32_t *plan,
-                    int32_t num_ctas, float *ws_o, float *ws_lse, int32_t ws_slots, void *out,
+                    int32_t num_ctas, void *ws_o, float *ws_lse, int32_t ws_slots, void *out,
                     int64_t out_stride_b, int64_t out_stride_h, float *lse, int64_t lse_stride_b,
                     void *stream);
 
 /*
  * The split step of mla_decode_bf16 alone (same arguments): requests covered
  * by one piece get their final bf16 output and LSE, split requests leave
- * normalised partials (fp32 outputs and LSE) in ws_o / ws_lse for mla_decode_merge_f32 with
+ * normalised partials (bf16 outputs, fp32 LSE) in ws_o / ws_lse for mla_decode_merge_f32 with
  * single_piece_final = 1. No counterpart in the reference (its decode is one
  * opaque library call); it is the unit a sequence-sharded decode distributes.
  */
@@ -167,18 +175,21 @@ int mla_decode_split_bf16(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                           const void *kv_pool, int64_t kv_row_stride, int32_t num_pages,
                           int32_t page_size, const int32_t *page_table, int64_t pt_stride,
                           const int32_t *seq_lens, int32_t batch, int32_t heads, float scale,
-                          const int32_t *plan, int32_t num_ctas, float *ws_o, float *ws_lse,
+                          const int32_t *plan, int32_t num_ctas, void *ws_o, float *ws_lse,
                           int32_t ws_slots, void *out, int64_t out_stride_b,
                           int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);
 
 /*
  * mla_decode_bf16 without a workspace argument: the split-KV partials go to a fixed scratch array
  * inside the library (static device memory, one copy per GPU, held until the process ends) of
- * MLA_NOALLOC_MAX_SLOT_HEADS slot-heads: 64 MiB of fp32 partials + 128 KiB of fp32 LSEs.
+ * MLA_NOALLOC_MAX_SLOT_HEADS slot-heads: 32 MiB of bf16 partials + 128 KiB of fp32 LSEs.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); it calls no
  * allocating routine. num_slots is the plan's slot count (mla_decode_plan's *num_slots); a plan
- * with num_slots * heads > MLA_NOALLOC_MAX_SLOT_HEADS is rejected with MLA_ERR_UNSUPPORTED. Every
+ * with num_slots * heads > MLA_NOALLOC_MAX_SLOT_HEADS is rejected with MLA_ERR_UNSUPPORTED. The
+ * scratch is laid out for 2 * num_ctas slots (the most any plan over num_ctas CTAs uses) whenever
+ * they fit, so a num_slots below the plan's real count cannot drop partials; if they do not fit
+ * and num_slots is too small, the merge writes NaN for the requests whose slots fall outside. Every
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent streams)
  * race. Nothing in the scratch must start at zero (the merge reads only slots the split kernel
  * of the same call wrote).
@@ -193,16 +204,17 @@ int mla_decode_bf16_noalloc(const void *q, int64_t q_stride_b, int64_t q_stride_
                             int64_t lse_stride_b, void *stream);
 
 /*
- * fp32 log-sum-exp merge of split-KV partials (fp32 ws_o and ws_lse; the merge step of
+ * fp32 log-sum-exp merge of split-KV partials (bf16 ws_o in the chunk order above, fp32 ws_lse; the
+ * merge step of
  * mla_decode_bf16). For request b with n = req_info[3b+1] pieces in slots
  * s = req_info[3b+2] .. +n-1:
  *   lse = ln sum_i exp(ws_lse[s_i]);  out = sum_i exp(ws_lse[s_i] - lse) * ws_o[s_i]
- * n == 0 writes out = 0, lse = -inf. With single_piece_final != 0 requests
+ * n == 0 writes out = 0, lse = -inf; slots outside [0, ws_slots) write NaN. With single_piece_final != 0 requests
  * with n == 1 are skipped (the split step already wrote them); otherwise
  * their one slot is converted like any other. More than 64 heads: the workspace holds one
  * [ws_slots, group heads, 512] block per 64-head group, as mla_decode_bf16 writes it.
  */
-int mla_decode_merge_f32(const float *ws_o, const float *ws_lse, int32_t ws_slots,
+int mla_decode_merge_f32(const void *ws_o, const float *ws_lse, int32_t ws_slots,
                          const int32_t *req_info, int32_t batch, int32_t heads,
                          int32_t single_piece_final, void *out, int64_t out_stride_b,
                          int64_t out_stride_h, float *lse, int64_t lse_stride_b, void *stream);

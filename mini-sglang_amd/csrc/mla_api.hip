@@ -7,6 +7,7 @@
 #include <limits.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include <string>
 
@@ -57,7 +58,7 @@ extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 8; }
+int mla_abi_version(void) { return 9; }
 
 int mla_device_cu_count(int device, int32_t* out) {
   if (out == nullptr) return fail(MLA_ERR_INVALID_ARG, "mla_device_cu_count: out is null");
@@ -276,7 +277,7 @@ static int check_out(const void* out, int64_t sb, int64_t sh, const float* lse, 
 static int decode_params(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          const void* kv_pool, int64_t kv_row_stride, int32_t num_pages, int32_t page_size,
                          const int32_t* page_table, int64_t pt_stride, const int32_t* seq_lens, int32_t batch,
-                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, float* ws_o,
+                         int32_t heads, float scale, const int32_t* plan, int32_t num_ctas, __bf16* ws_o,
                          float* ws_lse, int32_t ws_slots, void* out, int64_t out_stride_b, int64_t out_stride_h,
                          float* lse, int64_t lse_stride_b, mla::DecodeParams* p) {
   if (heads < 1 || heads > 64) return fail(MLA_ERR_UNSUPPORTED, "%s: heads must be in [1, 64], got %d", who, heads);
@@ -323,7 +324,7 @@ static int decode_params(const char* who, const void* q, int64_t q_stride_b, int
   return MLA_OK;
 }
 
-static mla::MergeParams merge_params(const float* ws_o, const float* ws_lse, int32_t ws_slots,
+static mla::MergeParams merge_params(const __bf16* ws_o, const float* ws_lse, int32_t ws_slots,
                                      const int32_t* req_info, int32_t batch, int32_t heads, int32_t skip_single,
                                      void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                                      int64_t lse_stride_b) {
@@ -351,14 +352,14 @@ constexpr int32_t kMaxHeads = 1024;
 
 struct HeadGroup {
   const void* q;
-  float* ws_o;
+  __bf16* ws_o;
   float* ws_lse;
   void* out;
   float* lse;
   int32_t heads;
 };
 
-static HeadGroup head_group(int32_t h0, int32_t heads, int32_t ws_slots, const void* q, int64_t q_stride_h, float* ws_o,
+static HeadGroup head_group(int32_t h0, int32_t heads, int32_t ws_slots, const void* q, int64_t q_stride_h, __bf16* ws_o,
                             float* ws_lse, void* out, int64_t out_stride_h, float* lse) {
   HeadGroup g;
   g.heads = heads - h0 < kHeadGroup ? heads - h0 : kHeadGroup;
@@ -382,7 +383,7 @@ static int check_head_groups(const char* who, int32_t heads, int64_t q_stride_b,
 int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                           int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                           int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                          const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                          const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
                           void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                           int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_split_bf16";
@@ -391,7 +392,7 @@ int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h,
   if (int rc = check_head_groups(who, heads, q_stride_b, q_stride_h, out_stride_b, out_stride_h, lse, lse_stride_b))
     return rc;
   for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {
-    const HeadGroup g = head_group(h0, heads, ws_slots, q, q_stride_h, ws_o, ws_lse, out, out_stride_h, lse);
+    const HeadGroup g = head_group(h0, heads, ws_slots, q, q_stride_h, static_cast<__bf16*>(ws_o), ws_lse, out, out_stride_h, lse);
     mla::DecodeParams p;
     if (int rc = decode_params(who, g.q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size,
                                page_table, pt_stride, seq_lens, batch, g.heads, scale, plan, num_ctas, g.ws_o,
@@ -405,17 +406,29 @@ int mla_decode_split_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 int mla_decode_bf16(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                     int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                     int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                    const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots,
+                    const int32_t* plan, int32_t num_ctas, void* ws_o, float* ws_lse, int32_t ws_slots,
                     void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b,
                     void* stream) {
   return mla::decode_split_merge("mla_decode_bf16", q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages,
                                  page_size, page_table, pt_stride, seq_lens, batch, heads, scale, plan, num_ctas,
-                                 ws_o, ws_lse, ws_slots, out, out_stride_b, out_stride_h, lse, lse_stride_b, stream);
+                                 static_cast<__bf16*>(ws_o), ws_lse, ws_slots, out, out_stride_b, out_stride_h, lse, lse_stride_b, stream);
 }
 
 }  // extern "C"
 
 namespace mla {
+
+int current_device_cus() {
+  static std::atomic<int> cus_of[64];  // zero-initialised; a value is written once, the same by every writer
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  int cus = dev < 64 ? cus_of[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev < 64) cus_of[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
 
 int api_error(int code, const char* fmt, ...) {
   char buf[512];
@@ -430,7 +443,7 @@ int api_error(int code, const char* fmt, ...) {
 int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                        int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                        int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                       const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots, void* out,
+                       const int32_t* plan, int32_t num_ctas, __bf16* ws_o, float* ws_lse, int32_t ws_slots, void* out,
                        int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   if (batch < 0) return fail(MLA_ERR_INVALID_ARG, "%s: batch < 0", who);
   if (batch == 0) return ok();
@@ -456,7 +469,7 @@ int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64
 
 extern "C" {
 
-int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
+int mla_decode_merge_f32(const void* ws_o, const float* ws_lse, int32_t ws_slots, const int32_t* req_info,
                          int32_t batch, int32_t heads, int32_t single_piece_final, void* out, int64_t out_stride_b,
                          int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream) {
   const char* who = "mla_decode_merge_f32";
@@ -467,7 +480,7 @@ int mla_decode_merge_f32(const float* ws_o, const float* ws_lse, int32_t ws_slot
   if (ws_o != nullptr && !aligned(ws_o, 16)) return fail(MLA_ERR_INVALID_ARG, "%s: ws_o must be 16-byte aligned", who);
   if (int rc = check_out(out, out_stride_b, out_stride_h, lse, lse_stride_b, heads, who)) return rc;
   for (int32_t h0 = 0; h0 < heads; h0 += kHeadGroup) {  // the workspace holds one [slots, group, 512] block per group
-    const HeadGroup g = head_group(h0, heads, ws_slots, nullptr, 0, const_cast<float*>(ws_o),
+    const HeadGroup g = head_group(h0, heads, ws_slots, nullptr, 0, static_cast<__bf16*>(const_cast<void*>(ws_o)),
                                    const_cast<float*>(ws_lse), out, out_stride_h, lse);
     const mla::MergeParams m = merge_params(g.ws_o, g.ws_lse, ws_slots, req_info, batch, g.heads,
                                             single_piece_final ? 1 : 0, g.out, out_stride_b, out_stride_h, g.lse,

@@ -48,7 +48,7 @@ struct DecodeParams {
   float scale_log2;  // softmax scale * log2(e)
   const int32_t* plan;  // [num_ctas * 4] ranges, then [batch * 3] request info
   int32_t num_ctas;
-  float* ws_o;    // [ws_slots, H, 512] normalised fp32 partial outputs
+  __bf16* ws_o;   // [ws_slots, H, 512] normalised bf16 partial outputs, chunk order of mla_amd.h
   float* ws_lse;  // [ws_slots, H]
   int32_t ws_slots;
   __bf16* out;  // [B, H, 512]
@@ -58,7 +58,7 @@ struct DecodeParams {
 };
 
 struct MergeParams {
-  const float* ws_o;  // fp32 partials
+  const __bf16* ws_o;  // bf16 partials, chunk order of mla_amd.h
   const float* ws_lse;
   int32_t ws_slots;
   const int32_t* req_info;  // [batch * 3]
@@ -105,9 +105,11 @@ struct PrefillParams {
 int decode_split_merge(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv_pool,
                        int64_t kv_row_stride, int32_t num_pages, int32_t page_size, const int32_t* page_table,
                        int64_t pt_stride, const int32_t* seq_lens, int32_t batch, int32_t heads, float scale,
-                       const int32_t* plan, int32_t num_ctas, float* ws_o, float* ws_lse, int32_t ws_slots, void* out,
+                       const int32_t* plan, int32_t num_ctas, __bf16* ws_o, float* ws_lse, int32_t ws_slots, void* out,
                        int64_t out_stride_b, int64_t out_stride_h, float* lse, int64_t lse_stride_b, void* stream);
 int api_error(int code, const char* fmt, ...);
+// Compute units of the current device (cached per device; safe from any host thread).
+int current_device_cus();
 
 hipError_t launch_prefill(const PrefillParams& p, int32_t total_q, hipStream_t stream);
 hipError_t launch_prefill_gather(const void* kv, int64_t kv_row_stride, int32_t num_pages, int32_t log2_ps,

@@ -14,11 +14,12 @@
 namespace {
 
 constexpr int64_t kMaxSlotHeads = MLA_NOALLOC_MAX_SLOT_HEADS;
-constexpr int64_t kPartialBytes = kMaxSlotHeads * MLA_V_DIM * 4;  // fp32 partial outputs
+constexpr int64_t kPartialBytes = kMaxSlotHeads * MLA_V_DIM * 2;  // bf16 partial outputs
 constexpr int64_t kScratchBytes = kPartialBytes + kMaxSlotHeads * 4;  // + fp32 LSEs
 static_assert(kPartialBytes % 256 == 0, "LSE block alignment");
 
-// [slot, head, 512] bf16 partial outputs, then [slot, head] fp32 LSEs (slot * heads <= kMaxSlotHeads)
+// [slot, head, 512] bf16 partial outputs (chunk order of mla_amd.h), then [slot, head] fp32 LSEs
+// (slot * heads <= kMaxSlotHeads)
 static __device__ __align__(256) char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -62,14 +63,21 @@ int mla_decode_bf16_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_
                           "%s: the plan's %d partial slots x %d heads exceed the fixed scratch of %lld slot-heads; "
                           "use mla_decode_bf16 with a workspace",
                           who, num_slots, heads, (long long)kMaxSlotHeads);
+  if (num_ctas < 1) return mla::api_error(MLA_ERR_INVALID_ARG, "%s: num_ctas must be >= 1", who);
   void* base = nullptr;
   if (int rc = scratch_address(&base)) return rc;
+  // A plan over num_ctas CTAs uses at most 2 * num_ctas slots (only a CTA's first and last piece can
+  // be part of a split request). Lay the scratch out for that many whenever they fit, so a num_slots
+  // below the plan's real count cannot make the split kernel drop partials; otherwise the merge
+  // flags slots past num_slots with NaN.
+  const int64_t most = 2 * (int64_t)num_ctas;
+  const int32_t ws_slots = most * heads <= kMaxSlotHeads ? (int32_t)most : num_slots;
   // every slot the merge reads is written by the split kernel of the same call: nothing to clear
-  float* ws_o = static_cast<float*>(base);
+  __bf16* ws_o = static_cast<__bf16*>(base);
   float* ws_lse = reinterpret_cast<float*>(static_cast<char*>(base) + kPartialBytes);
   return mla::decode_split_merge(who, q, q_stride_b, q_stride_h, kv_pool, kv_row_stride, num_pages, page_size,
                                  page_table, pt_stride, seq_lens, batch, heads, scale, plan, num_ctas, ws_o, ws_lse,
-                                 num_slots, out, out_stride_b, out_stride_h, lse, lse_stride_b, stream);
+                                 ws_slots, out, out_stride_b, out_stride_h, lse, lse_stride_b, stream);
 }
 
 }  // extern "C"

@@ -759,15 +759,7 @@ hipError_t launch_prefill(const PrefillParams& p0, int32_t total_q, hipStream_t 
   // compute units at least eight times over; a smaller batch keeps one head per CTA, whose finer
   // grain the hardware's CTA scheduling balances better (a 64-head prefill of one 256-row block
   // takes twice as long with two heads per CTA).
-  static int cus_of[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  int cus = dev >= 0 && dev < 64 ? cus_of[dev] : 0;
-  if (cus <= 0) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (dev >= 0 && dev < 64) cus_of[dev] = cus;
-  }
-  if (blocks * p0.heads >= 8LL * cus)
+  if (blocks * p0.heads >= 8LL * current_device_cus())
     hipLaunchKernelGGL((mla_prefill_kernel<kPrefillQS, 2>), dim3((unsigned)(blocks * ((p0.heads + 1) / 2))),
                        dim3(8 / kPrefillQS * 64), 0, stream, p0);
   else

@@ -53,6 +53,42 @@ def prefill_scratch_bytes(num_heads: int, rows: int) -> int:
     return rows * (num_heads * 256 + 64 + 512) * 2
 
 
+def decode_workspace_bytes(num_heads: int, slots: int) -> int:
+    """Device bytes of a decode workspace of ``slots`` split-KV slots: a bf16 partial row of 512 dims
+    and an fp32 LSE per (slot, head)."""
+    return slots * num_heads * (512 * 2 + 4)
+
+
+def plan_grid_bound(num_ctas: int, tokens: int, reqs: int) -> int:
+    """Smallest ``num_ctas * 2^k`` plan grid that holds any batch of ``reqs`` requests and ``tokens``
+    tokens in all: the planner closes a CTA range only at ``MAX_CTA_BLOCKS`` blocks or
+    ``MAX_CTA_REQUESTS`` requests (pieces have no length limit), and each request rounds up by less
+    than one block."""
+    blocks = -(-tokens // lib.PLAN_BLOCK) + reqs
+    need = -(-blocks // lib.MAX_CTA_BLOCKS) + -(-reqs // (lib.MAX_CTA_REQUESTS - 1)) + 1
+    grid = num_ctas
+    while grid < need:
+        grid *= 2
+    return grid
+
+
+def backend_device_bytes(num_heads: int, num_ctas: int, max_running_req: int, max_seq_len: int,
+                         prefill_scratch_rows: int = DEFAULT_PREFILL_SCRATCH_ROWS, graph_max_bs: int = 0) -> int:
+    """Device memory an ``MLAAttnBackend`` holds beside the KV pool, for an engine to subtract before
+    it sizes the pool (``python/minisgl/engine/engine.py:148-165`` sizes the pool from the free
+    memory before the backend exists): the prefill decompression scratch, the eager decode
+    workspace for the largest plan grid a batch of ``max_running_req`` requests of at most
+    ``max_seq_len`` tokens can need, and -- with graphs up to ``graph_max_bs`` requests -- the
+    captured graphs' workspace and plan. A plan uses at most 2 slots per CTA range."""
+    eager = plan_grid_bound(num_ctas, max_running_req * max_seq_len, max_running_req)
+    total = prefill_scratch_bytes(num_heads, prefill_scratch_rows) + decode_workspace_bytes(num_heads, 2 * eager)
+    if graph_max_bs > 0:
+        graph = plan_grid_bound(num_ctas, graph_max_bs * max_seq_len, graph_max_bs)
+        total += decode_workspace_bytes(num_heads, 2 * graph)
+        total += 4 * (graph * lib.PLAN_CTA_INTS + graph_max_bs * lib.PLAN_REQ_INTS)
+    return total
+
+
 def prefill_passes(seqlens_k: List[int], cap_rows: int) -> List[Tuple[int, int, List[int]]]:
     """Split a prefill batch into passes of consecutive whole requests whose keys fit ``cap_rows``
     scratch rows (each request rounded up to 64-row pages); a request longer than the scratch is a
@@ -103,7 +139,11 @@ class MLAMetadata(BaseAttnMetadata):
 
 class MLAAttnBackend(BaseAttnBackend):
     def __init__(self, config: MLAConfig, num_ctas: int | None = None,
-                 prefill_scratch_rows: int = DEFAULT_PREFILL_SCRATCH_ROWS):
+                 prefill_scratch_rows: int = DEFAULT_PREFILL_SCRATCH_ROWS, reserve_scratch: bool = False):
+        """``reserve_scratch`` allocates the prefill decompression scratch (``prefill_scratch_rows``
+        keys) and the eager decode workspace here, as the reference's FlashInfer backend allocates
+        its workspace in its constructor (``attention/fi.py:90-92``); otherwise they are allocated at
+        the first batch that needs them. ``backend_device_bytes`` gives their size beforehand."""
         ctx = get_global_ctx()
         assert isinstance(ctx.kv_cache, MLAKVCache), "the MLA backend needs an MLAKVCache pool"
         self.config = config
@@ -116,8 +156,6 @@ class MLAAttnBackend(BaseAttnBackend):
             dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
             num_ctas = lib.device_cu_count(dev_index)
         self.num_ctas = num_ctas
-        # every batch's tokens live in the pool, which bounds the grid a decode plan can need
-        self.pool_tokens = self.kvcache.num_pages * self.page_size
         self.capture: MLACaptureData | None = None
         self.capture_bs: List[int] = []
         self.max_graph_bs = 0
@@ -126,6 +164,12 @@ class MLAAttnBackend(BaseAttnBackend):
         # fixed from init_capture_graph, so an eager batch never resizes memory a graph points at
         self.ws_eager: Tuple[torch.Tensor, torch.Tensor] | None = None
         self.ws_graph: Tuple[torch.Tensor, torch.Tensor] | None = None
+        # the eager workspace's last use: an event recorded on the stream of the decode that used it.
+        # prepare_metadata of the next batch can run on another stream while that decode still writes
+        # partials (python/minisgl/scheduler/scheduler.py:98-103); a workspace replaced by a larger one
+        # is kept (retired) until its event has completed, so its memory is not handed out meanwhile
+        self.ws_eager_fence = None
+        self.ws_retired: List[tuple] = []
         self.last_lse: torch.Tensor | None = None  # natural-log LSE of the last forward
         # prefill decompression: the layers' W_kvb [H * (128 + 128), 512] and a scratch of
         # prefill_scratch_rows keys (allocated at the first prefill, grown for a longer request)
@@ -134,18 +178,25 @@ class MLAAttnBackend(BaseAttnBackend):
         self.kv_b: dict = {}
         self.scratch_rows: torch.Tensor | None = None  # [rows, H * 256 + 64]: [k_nope | v] per head, rope
         self.scratch_c: torch.Tensor | None = None  # [rows, 512] latent dims (the GEMM input)
+        if reserve_scratch:
+            self._prefill_scratch(prefill_scratch_rows)
+            self._eager_workspace(2 * self.num_ctas)
 
     # ------------------------------------------------------------------ workspace
     def _new_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
         capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
         assert not capturing, "decode workspaces are allocated outside capture"
-        ws_o = torch.empty((slots, self.num_heads, self.config.kv_lora_rank), dtype=torch.float32, device=self.device)
-        ws_lse = torch.empty((slots, self.num_heads), dtype=torch.float32, device=self.device)
-        return ws_o, ws_lse
+        assert self.config.kv_lora_rank == 512
+        return lib.decode_workspace(slots, self.num_heads, self.device)
 
     def _eager_workspace(self, slots: int) -> Tuple[torch.Tensor, torch.Tensor]:
         if self.ws_eager is None or self.ws_eager[0].shape[0] < slots:
+            if self.ws_eager is not None and self.ws_eager_fence is not None:
+                self.ws_retired.append((self.ws_eager, self.ws_eager_fence))
             self.ws_eager = self._new_workspace(max(slots, 2 * self.num_ctas))
+            self.ws_eager_fence = None
+        # drop retired workspaces whose last decode has completed
+        self.ws_retired = [(ws, ev) for ws, ev in self.ws_retired if not ev.query()]
         return self.ws_eager
 
     # ------------------------------------------------------------------ forward
@@ -173,6 +224,10 @@ class MLAAttnBackend(BaseAttnBackend):
             q, self.kvcache.latent_cache(layer_id), metadata.page_table, metadata.cache_seqlens, metadata.plan,
             metadata.num_ctas, ws_o, ws_lse, self.scale, out, lse,
         )
+        if self.ws_eager is not None and ws_o is self.ws_eager[0] and not torch.cuda.is_current_stream_capturing():
+            if self.ws_eager_fence is None:
+                self.ws_eager_fence = torch.cuda.Event()
+            self.ws_eager_fence.record()  # on the current (engine) stream, after this decode
         self.last_lse = lse
         return out
 
@@ -222,7 +277,7 @@ class MLAAttnBackend(BaseAttnBackend):
         rounds). With ``grid`` the plan is laid out for a launch of ``grid`` CTAs: the CTAs past the
         planned ones get empty ranges. Returns ``(plan, slots, launch CTAs)``."""
         ctas = self.num_ctas
-        limit = grid if grid is not None else max(self.num_ctas, self._grid_bound(sum(seqlens_k), len(seqlens_k)))
+        limit = grid if grid is not None else max(self.num_ctas, plan_grid_bound(self.num_ctas, sum(seqlens_k), len(seqlens_k)))
         while True:
             try:
                 plan_np, slots = lib.decode_plan(seqlens_k, self.page_size, ctas)
@@ -235,18 +290,6 @@ class MLAAttnBackend(BaseAttnBackend):
         if grid is None or grid == ctas:
             return plan_np, slots, ctas
         return pad_plan(plan_np, ctas, grid, len(seqlens_k)), slots, grid
-
-    def _grid_bound(self, tokens: int, reqs: int) -> int:
-        """Smallest ``num_ctas * 2^k`` grid that holds any batch of ``reqs`` requests and ``tokens``
-        tokens in all: the planner closes a CTA only at ``MAX_CTA_BLOCKS`` blocks or
-        ``MAX_CTA_REQUESTS`` requests (pieces have no length limit), and each request rounds up by
-        less than one block."""
-        blocks = -(-tokens // lib.PLAN_BLOCK) + reqs
-        need = -(-blocks // lib.MAX_CTA_BLOCKS) + -(-reqs // (lib.MAX_CTA_REQUESTS - 1)) + 1
-        grid = self.num_ctas
-        while grid < need:
-            grid *= 2
-        return grid
 
     # ------------------------------------------------------------------ metadata
     def prepare_metadata(self, batch: Batch) -> None:
@@ -320,9 +363,13 @@ class MLAAttnBackend(BaseAttnBackend):
         assert self.capture is None, "Capture already initialized."
         max_bs = max(bs_list)
         cols = -(-max_seq_len // self.page_size)
-        # the captured launch has a fixed grid: the one the largest batch the graphs can replay needs,
-        # whose tokens are bounded by both the pool and max_bs * max_seq_len
-        self.capture_ctas = self._grid_bound(min(self.pool_tokens, max_bs * max_seq_len), max_bs)
+        # the captured launch has a fixed plan grid: the one the largest batch the graphs can replay
+        # needs. Its tokens are bounded by max_bs * max_seq_len, not by the pool: requests sharing
+        # prefix pages (the radix cache) can hold more tokens in all than the pool has. The kernels
+        # run a plan of more ranges than compute units as a loop over ranges (the launch grid stays
+        # at one CTA per compute unit) and stop at the first padding range, so a large plan grid costs
+        # only its workspace (2 slots per range)
+        self.capture_ctas = plan_grid_bound(self.num_ctas, max_bs * max_seq_len, max_bs)
         plan = torch.zeros((self.capture_ctas * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS,), dtype=torch.int32,
                            device=self.device)
         self.ws_graph = self._new_workspace(2 * self.capture_ctas)  # a plan needs at most 2 slots per CTA

@@ -78,12 +78,31 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 PLAN_BLOCK = 64
 PLAN_CTA_INTS = 4
 PLAN_REQ_INTS = 3
 MAX_CTA_BLOCKS = 512
 MAX_CTA_REQUESTS = 128
+
+
+def partial_chunk_dims():
+    """Value dim held at each of the 512 positions of a split-KV partial row (the chunk order of
+    ``include/mla_amd.h``): 16-byte chunk c holds dims 32 (c // 4) + 4 (c % 4) + {0..3}, then the
+    same + 16."""
+    c = np.arange(64)[:, None]
+    e = np.arange(8)[None, :]
+    return (32 * (c // 4) + 4 * (c % 4) + (e % 4) + 16 * (e // 4)).reshape(-1)
+
+
+def decode_workspace(slots: int, heads: int, device):
+    """Split-KV workspace for ``slots`` partial slots: ``ws_o [slots, heads, 512]`` bf16 and
+    ``ws_lse [slots, heads]`` fp32 (at least one slot, so the pointers are valid)."""
+    import torch
+
+    n = max(int(slots), 1)
+    return (torch.empty((n, heads, 512), dtype=torch.bfloat16, device=device),
+            torch.empty((n, heads), dtype=torch.float32, device=device))
 
 
 class MLAKernelError(RuntimeError):
@@ -217,7 +236,7 @@ def mla_decode(
     ws_slots = 0 if ws_o is None else ws_o.shape[0]
     if ws_o is not None:
         assert ws_o.shape[1:] == (H, 512) and ws_lse.shape[:2] == (ws_slots, H)
-        assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32
+        assert ws_o.dtype == torch.bfloat16 and ws_lse.dtype == torch.float32, "ws_o is bf16, ws_lse fp32"
     if lse is not None:
         assert lse.dtype == torch.float32 and lse.shape == (B, H) and lse.stride(-1) == 1
     fn = load_library().mla_decode_split_bf16 if split_only else load_library().mla_decode_bf16
@@ -262,10 +281,11 @@ def mla_decode_noalloc(q, kv_pool, page_table, seq_lens, plan, num_ctas: int, nu
 
 
 def mla_decode_merge(ws_o, ws_lse, req_info, out, lse=None, stream=None, single_piece_final: bool = False) -> None:
-    """fp32 LSE merge of partials ``ws_o [S, H, 512]`` / ``ws_lse [S, H]`` (both fp32) per ``req_info``."""
+    """fp32 LSE merge of partials ``ws_o [S, H, 512]`` (bf16, chunk order of ``partial_chunk_dims``) /
+    ``ws_lse [S, H]`` (fp32) per ``req_info``."""
     import torch
 
-    assert ws_o.dtype == torch.float32 and ws_lse.dtype == torch.float32, "ws_o and ws_lse are fp32"
+    assert ws_o.dtype == torch.bfloat16 and ws_lse.dtype == torch.float32, "ws_o is bf16, ws_lse fp32"
     B, H = out.shape[0], out.shape[1]
     check(
         load_library().mla_decode_merge_f32(

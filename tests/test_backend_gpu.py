@@ -338,3 +338,40 @@ def test_backend_decode_page_size_one_kimi_batch():
     torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
     torch.testing.assert_close(backend.last_lse.cpu(), lse_ref, **LSE_TOL)
     reset_global_ctx()
+
+
+def test_backend_reserves_the_bytes_it_reports():
+    """An engine sizes the pool from the free memory before the backend exists
+    (python/minisgl/engine/engine.py:148-165): backend_device_bytes gives the backend's own device
+    memory beforehand, and with reserve_scratch the constructor allocates the prefill scratch and
+    the eager decode workspace at once, within that figure; a decode and a prefill afterwards
+    allocate no further scratch or workspace."""
+    from minisgl_amd.attention.mla import (MLAAttnBackend, backend_device_bytes, decode_workspace_bytes,
+                                           prefill_scratch_bytes)
+    from minisgl_amd.kernel import lib
+
+    cus = lib.device_cu_count(0)
+    H, rows, max_req, max_seq_len = 64, 8192, 8, 4096
+    reserve = backend_device_bytes(H, cus, max_req, max_seq_len, prefill_scratch_rows=rows)
+    ctx, cfg, pool, _, reqs, tt, _ = _setup(max_req=max_req, max_seq_len=max_seq_len)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(DEV)
+    backend = MLAAttnBackend(cfg, prefill_scratch_rows=rows, reserve_scratch=True)
+    held = torch.cuda.memory_allocated(DEV) - before
+    expect = prefill_scratch_bytes(H, rows) + decode_workspace_bytes(H, 2 * cus)
+    assert expect <= held <= reserve + 4096, (held, expect, reserve)
+    ctx.attn_backend = backend
+    ws, scratch = backend.ws_eager[0], backend.scratch_rows
+    gen = torch.Generator().manual_seed(3)
+    batch = Batch(reqs=reqs, phase="decode")
+    batch.padded_reqs = reqs
+    batch.out_loc = torch.tensor([int(tt[r.table_idx, r.device_len - 1]) for r in reqs], dtype=torch.int32, device=DEV)
+    backend.prepare_metadata(batch)
+    q = torch.randn((len(reqs), H, 576), generator=gen).to(torch.bfloat16).to(DEV)
+    k_new = torch.randn((len(reqs), 576), generator=gen).to(torch.bfloat16).to(DEV)
+    with ctx.forward_batch(batch):
+        o = backend.forward(q, k_new, k_new[:, :512], 0, batch)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = _expected(pool, tt, reqs, q, 0, ctx.page_size)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    assert backend.ws_eager[0] is ws and backend.scratch_rows is scratch

@@ -29,8 +29,7 @@ def run_decode(q, kv, pt, seq_lens, lens, ps, num_ctas, scale=R.DEFAULT_SCALE):
     B, H, _ = q.shape
     plan_np, slots = lib.decode_plan(lens, ps, num_ctas)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=DEV)
-    ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=DEV)
+    ws_o, ws_lse = lib.decode_workspace(slots, H, DEV)
     out = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
     lse = torch.full((B, H), float("nan"), dtype=torch.float32, device=DEV)
     lib.mla_decode(q, kv, pt, seq_lens, plan, num_ctas, ws_o, ws_lse, scale, out, lse)
@@ -83,8 +82,7 @@ def test_decode_tensor_parallel_head_counts(heads, ps):
     B = len(case.lens)
     plan_np, slots = lib.decode_plan(case.lens, ps, 3)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.float32, device=DEV)
-    ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
+    ws_o, ws_lse = lib.decode_workspace(slots, heads, DEV)
     wide = torch.full((B, heads + 1, 512), 7.0, dtype=torch.bfloat16, device=DEV)
     wide_lse = torch.full((B, heads + 1), 7.0, dtype=torch.float32, device=DEV)
     lib.mla_decode(case.q.to(DEV), case.kv_pool.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV), plan, 3,
@@ -110,8 +108,7 @@ def test_decode_whole_head_groups(heads, ps, num_ctas):
     q, kv, pt, sl = case.q.to(DEV), case.kv_pool.to(DEV), case.page_table.to(DEV), case.seq_lens.to(DEV)
     outs = []
     for two_step in (False, True):
-        ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.float32, device=DEV)
-        ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
+        ws_o, ws_lse = lib.decode_workspace(slots, heads, DEV)
         out = torch.empty((B, heads, 512), dtype=torch.bfloat16, device=DEV)
         lse = torch.empty((B, heads), dtype=torch.float32, device=DEV)
         lib.mla_decode(q, kv, pt, sl, plan, num_ctas, ws_o, ws_lse, R.DEFAULT_SCALE, out, lse, split_only=two_step)
@@ -146,6 +143,43 @@ def test_decode_kimi_k2_full_batch():
     o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
     torch.testing.assert_close(out, o_ref, **O_TOL)
     torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
+
+
+@pytest.mark.parametrize("num_ctas", [512, 1024])
+def test_decode_kimi_k2_more_ranges_than_compute_units(num_ctas):
+    """The benchmark's batch planned over 512 / 1024 CTA ranges (the warp-specialized kernel): the
+    launch keeps one CTA per compute unit and each CTA runs its ranges w, w + 256, ... in turn."""
+    case = make_decode_case(64, 64, 64, len_range=(1024, 8192), device=DEV, seed=4)
+    out, lse, slots = run_decode(case.q, case.kv_pool, case.page_table, case.seq_lens, case.lens, 64, num_ctas)
+    assert slots > 2 * 256
+    o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
+    torch.testing.assert_close(out, o_ref, **O_TOL)
+    torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
+
+
+@pytest.mark.parametrize("heads,ps", [(64, 64), (16, 1)])
+def test_decode_padded_plan(heads, ps):
+    """A plan made for 256 ranges laid out for 2048 (as for a captured graph): the kernels stop each
+    CTA's loop at the first padding range; same bits as the unpadded plan."""
+    from minisgl_amd.attention.mla import pad_plan
+
+    case = make_decode_case(12, heads, ps, len_range=(1, 9000), device=DEV, seed=6)
+    B = len(case.lens)
+    plan_np, slots = lib.decode_plan(case.lens, ps, 256)
+    outs = []
+    for grid, pl in ((256, plan_np), (2048, pad_plan(plan_np, 256, 2048, B))):
+        ws_o, ws_lse = lib.decode_workspace(slots, heads, DEV)
+        out = torch.full((B, heads, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
+        lse = torch.full((B, heads), float("nan"), dtype=torch.float32, device=DEV)
+        lib.mla_decode(case.q, case.kv_pool, case.page_table, case.seq_lens, torch.from_numpy(pl).to(DEV), grid,
+                       ws_o, ws_lse, R.DEFAULT_SCALE, out, lse)
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), lse.cpu()))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1], outs[1][1])
+    o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
+    torch.testing.assert_close(outs[0][0].float(), o_ref, **O_TOL)
+    torch.testing.assert_close(outs[0][1], lse_ref, **LSE_TOL)
 
 
 def test_decode_one_long_request_over_every_cta():
@@ -198,18 +232,19 @@ def test_decode_64_heads_page_sizes(ps, num_ctas):
 
 
 def test_merge_kernel_standalone():
-    """fp32 partials, fp32 merge, one rounding to bf16: every output element lies within half a bf16
-    ulp of the float64 merge (plus fp32 accumulation slack). bf16 partials (a second rounding) would
-    break this bound."""
+    """bf16 partials (in the chunk order of mla_amd.h), fp32 merge, one rounding to bf16: every output
+    element lies within half a bf16 ulp of the float64 merge of those partials (plus fp32
+    accumulation slack), so the merge rounds once and reads every dim from its chunk position."""
     gen = torch.Generator().manual_seed(5)
     H, S = 16, 11
-    o_parts = torch.randn((S, H, 512), generator=gen)  # partials are fp32
+    o_parts = torch.randn((S, H, 512), generator=gen).to(torch.bfloat16).double()  # the bf16 partials
     lse_parts = torch.randn((S, H), generator=gen) * 3
     lse_parts[4] = float("-inf")  # an empty piece
     req_info = torch.tensor([[0, 3, 0], [0, 1, 3], [0, 0, 0], [0, 7, 4]], dtype=torch.int32)
     out = torch.empty((4, H, 512), dtype=torch.bfloat16, device=DEV)
     lse = torch.empty((4, H), dtype=torch.float32, device=DEV)
-    lib.mla_decode_merge(o_parts.to(DEV), lse_parts.to(DEV), req_info.flatten().to(DEV), out, lse)
+    ws_o = o_parts[..., torch.from_numpy(lib.partial_chunk_dims())].to(torch.bfloat16)  # chunk order
+    lib.mla_decode_merge(ws_o.to(DEV), lse_parts.to(DEV), req_info.flatten().to(DEV), out, lse)
     torch.cuda.synchronize()
     for b, (_, n, base) in enumerate(req_info.tolist()):
         o_ref, l_ref = R.mla_merge(o_parts[base : base + n].double(), lse_parts[base : base + n].double())
@@ -267,8 +302,7 @@ def test_split_then_merge_equals_one_call(heads):
     q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
     plan_np, slots = lib.decode_plan(case.lens, 64, 32)
     plan = torch.from_numpy(plan_np).to(DEV)
-    ws_o = torch.empty((max(slots, 1), heads, 512), dtype=torch.float32, device=DEV)
-    ws_lse = torch.empty((max(slots, 1), heads), dtype=torch.float32, device=DEV)
+    ws_o, ws_lse = lib.decode_workspace(slots, heads, DEV)
     outs = []
     for two_step in (False, True):
         out = torch.empty((6, heads, 512), dtype=torch.bfloat16, device=DEV)

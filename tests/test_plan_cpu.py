@@ -90,7 +90,7 @@ def test_plan_rejects_impossible():
         lib.decode_plan([1] * (lib.MAX_CTA_REQUESTS + 1), 64, 1)
 
 
-def _backend(ps, pool_tokens=None, num_ctas=256):
+def _backend(ps, num_ctas=256):
     import torch
 
     from minisgl_amd.attention.mla import MLAAttnBackend
@@ -103,8 +103,6 @@ def _backend(ps, pool_tokens=None, num_ctas=256):
     set_global_ctx(ctx)
     ctx.kv_cache = create_kvcache_pool(MLAConfig(num_layers=1, num_heads=16), 4, ps, torch.bfloat16, "cpu")
     be = MLAAttnBackend(MLAConfig(num_layers=1, num_heads=16), num_ctas=num_ctas)
-    if pool_tokens is not None:  # stands for a large pool without allocating it
-        be.pool_tokens = pool_tokens
     reset_global_ctx()
     return be
 
@@ -123,26 +121,38 @@ def test_backend_plans_kimi_batch_on_one_round(ps):
 
 @pytest.mark.parametrize("ps", [1, 64])
 @pytest.mark.parametrize("max_bs", [160, 256])
-def test_capture_grid_is_bounded_by_the_pool(ps, max_bs):
+def test_capture_grid_holds_any_replayable_batch(ps, max_bs):
     """init_capture_graph at the reference's defaults (max_seq_len 131072, graph batch sizes up to
-    160 / 256, python/minisgl/engine/graph.py:58-62) sizes the captured grid from the pool's token
-    capacity, not max_bs * max_seq_len; replayed batches are planned on the smallest grid that
-    fits and padded with empty CTAs; eager batches larger than every graph (256 requests, the
-    reference's max_running_req) plan on their own workspace."""
-    be = _backend(ps, pool_tokens=2_000_000)
+    160 / 256, python/minisgl/engine/graph.py:58-62) sizes the captured plan grid from max_bs *
+    max_seq_len, not from the pool: requests that share radix-cache prefix pages can hold more
+    tokens in all than the pool has, and every replayable batch must plan on the captured grid.
+    Replayed batches are padded with empty ranges; eager batches plan on their own workspace."""
+    be = _backend(ps)
     bs_list = [1, 2, 4] + list(range(8, max_bs + 1, 8))
     be.init_capture_graph(max_seq_len=131072, bs_list=bs_list)
-    assert be.capture_ctas == 256
+    assert be.capture_ctas * lib.MAX_CTA_BLOCKS * lib.PLAN_BLOCK >= max_bs * 131072
+    assert be.capture_ctas == {160: 1024, 256: 2048}[max_bs]
     graph_ws = be.ws_graph[0]
     assert graph_ws.shape[0] == 2 * be.capture_ctas
+    pool_tokens = be.kvcache.num_pages * ps
     rng = np.random.default_rng(ps)
-    lens = rng.integers(1024, 8193, size=max_bs).tolist()
+    # shared-prefix batch: every request 100k-131k tokens long (far more tokens than the pool holds)
+    lens = rng.integers(100_000, 131_073, size=max_bs).tolist()
+    assert sum(lens) > 2_000_000 > pool_tokens
     plan, slots, grid = be._plan(lens, be.capture_ctas)
     assert grid == be.capture_ctas and slots <= graph_ws.shape[0]
     assert plan.shape[0] == grid * lib.PLAN_CTA_INTS + max_bs * lib.PLAN_REQ_INTS
     pieces = plan_pieces(plan, grid, lens)
     assert sum(t1 - t0 for *_, t0, t1 in pieces) == sum(lens)
-    # a replayed batch with few tokens: the same grid, the CTAs past the planned ones empty
+    # the Kimi-K2 decode batch replayed: the same grid, the ranges past the planned ones empty
+    lens = rng.integers(1024, 8193, size=max_bs).tolist()
+    plan, slots, grid = be._plan(lens, be.capture_ctas)
+    assert grid == be.capture_ctas
+    cta = plan[: grid * 4].reshape(grid, 4)
+    used = int((cta[:, 0] < max_bs).sum())
+    assert used <= 256 and (cta[used:] == np.array([max_bs, 0, max_bs, 0])).all()
+    assert sum(t1 - t0 for *_, t0, t1 in plan_pieces(plan, grid, lens)) == sum(lens)
+    # a replayed batch with few tokens
     plan, slots, grid = be._plan([1] * 8, be.capture_ctas)
     cta = plan[: grid * 4].reshape(grid, 4)
     assert (cta[8:] == np.array([8, 0, 8, 0])).all()
@@ -153,17 +163,63 @@ def test_capture_grid_is_bounded_by_the_pool(ps, max_bs):
     assert ws[0].shape[0] >= slots and be.ws_graph[0] is graph_ws
 
 
-def test_capture_grid_grows_with_a_huge_pool():
-    """A pool whose batches can pass 256 CTAs x MAX_CTA_BLOCKS blocks doubles the captured grid."""
-    be = _backend(1, pool_tokens=40_000_000)
-    be.init_capture_graph(max_seq_len=131072, bs_list=[1, 160])
-    # 160 x 131072 = 21M tokens = 327680 blocks: more than 256 (and 512) CTAs x MAX_CTA_BLOCKS
-    assert be.capture_ctas == 1024 and lib.MAX_CTA_BLOCKS == 512
-    assert be.capture_ctas * lib.MAX_CTA_BLOCKS * lib.PLAN_BLOCK >= 160 * 131072
-    rng = np.random.default_rng(7)
-    lens = rng.integers(100_000, 131_073, size=160).tolist()
-    plan, slots, grid = be._plan(lens, be.capture_ctas)
-    assert grid == 1024 and sum(t1 - t0 for *_, t0, t1 in plan_pieces(plan, grid, lens)) == sum(lens)
+def test_capture_plan_padding_is_a_suffix():
+    """The kernels stop a CTA's loop over ranges w, w + grid, ... at the first padding range: the
+    padding of a plan laid out for a larger grid must be the suffix of the ranges, and no range
+    before it may be empty-by-padding."""
+    be = _backend(64)
+    be.init_capture_graph(max_seq_len=131072, bs_list=[1, 64, 160])
+    rng = np.random.default_rng(3)
+    for B in (1, 64, 160):
+        lens = rng.integers(1, 131_073, size=B).tolist()
+        plan, _, grid = be._plan(lens, be.capture_ctas)
+        first = plan[: grid * 4].reshape(grid, 4)[:, 0]
+        pad = np.nonzero(first >= B)[0]
+        assert len(pad) == 0 or (pad == np.arange(pad[0], grid)).all()
+
+
+def test_backend_device_bytes():
+    """backend_device_bytes: what the backend holds beside the pool, known before the pool is sized."""
+    from minisgl_amd.attention.mla import backend_device_bytes, decode_workspace_bytes, prefill_scratch_bytes
+
+    H = 64
+    b = backend_device_bytes(H, 256, max_running_req=256, max_seq_len=131072, prefill_scratch_rows=65536)
+    # 256 x 131072 tokens need 2048 plan ranges: 4096 slots
+    assert b == prefill_scratch_bytes(H, 65536) + decode_workspace_bytes(H, 4096)
+    assert decode_workspace_bytes(H, 1) == H * (1024 + 4)
+    g = backend_device_bytes(H, 256, 256, 131072, 65536, graph_max_bs=160)
+    assert g == b + decode_workspace_bytes(H, 2048) + 4 * (1024 * 4 + 160 * 3)
+
+
+def test_retired_eager_workspace_is_kept_until_its_decode_completes():
+    """A grown eager workspace replaces the old one only in the backend's bookkeeping: the old buffers
+    stay referenced until the event recorded after the decode that last used them has completed."""
+    import torch
+
+
+    class Fence:
+        def __init__(self):
+            self.done = False
+
+        def query(self):
+            return self.done
+
+    be = _backend(64)
+    ws_a = be._eager_workspace(10)
+    assert ws_a[0].shape[0] == 2 * be.num_ctas and ws_a[0].dtype == torch.bfloat16
+    fence = Fence()
+    be.ws_eager_fence = fence  # what forward records after a decode on ws_a
+    ws_b = be._eager_workspace(10 * be.num_ctas)  # growth
+    assert ws_b[0] is not ws_a[0] and ws_b[0].shape[0] == 10 * be.num_ctas
+    assert len(be.ws_retired) == 1 and be.ws_retired[0][0][0] is ws_a[0], "the old workspace is fenced"
+    be._eager_workspace(5)
+    assert len(be.ws_retired) == 1, "still in use: kept"
+    fence.done = True
+    be._eager_workspace(5)
+    assert be.ws_retired == [], "its decode completed: released"
+    # a workspace that no decode used (no fence) is released at once
+    be._eager_workspace(20 * be.num_ctas)
+    assert be.ws_retired == []
 
 
 def test_prefill_passes_hold_whole_requests_within_the_scratch():

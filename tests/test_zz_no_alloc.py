@@ -21,8 +21,7 @@ def _both(case, num_ctas):
     plan_np, slots = lib.decode_plan(case.lens, case.page_size, num_ctas)
     plan = torch.from_numpy(plan_np).to(DEV)
     q, kv, pt, sl = (t.to(DEV) for t in (case.q, case.kv_pool, case.page_table, case.seq_lens))
-    ws_o = torch.empty((max(slots, 1), H, 512), dtype=torch.float32, device=DEV)
-    ws_lse = torch.empty((max(slots, 1), H), dtype=torch.float32, device=DEV)
+    ws_o, ws_lse = lib.decode_workspace(slots, H, DEV)
     out_a = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
     lse_a = torch.full((B, H), float("nan"), dtype=torch.float32, device=DEV)
     lib.mla_decode(q, kv, pt, sl, plan, num_ctas, ws_o, ws_lse, R.DEFAULT_SCALE, out_a, lse_a)
