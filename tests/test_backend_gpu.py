@@ -253,6 +253,25 @@ def test_backend_prefill_in_passes():
     reset_global_ctx()
 
 
+def test_backend_prefill_many_requests():
+    """130 prefill requests in one batch through the backend (extends 1..300 on cached prefixes
+    0..900): more requests than one 64-request chunk of the kernel's work-item scan, decompressed
+    from the latent pool and checked against the oracle."""
+    H = 8
+    g = torch.Generator().manual_seed(13)
+    n = 130
+    extends = torch.randint(1, 301, (n,), generator=g).tolist()
+    cached = torch.randint(0, 901, (n,), generator=g).tolist()
+    cached[:3], extends[:3] = [0, 500, 0], [1, 1, 300]
+    ctx, pool, backend, tt, lens, kv_b, gen = _prefill_setup(64, cached, extends, H, seed=13)
+    o, lse, batch, q = _run_prefill(ctx, pool, backend, tt, cached, extends, kv_b, gen, H=H)
+    (o_ref, lse_ref), cu = _prefill_expected(pool, tt, cached, extends, kv_b, q, 1, 64, H)
+    torch.testing.assert_close(o.float().cpu(), o_ref, **O_TOL)
+    torch.testing.assert_close(lse.cpu(), lse_ref, **LSE_TOL)
+    assert torch.equal(batch.attn_metadata.get_last_indices(n).cpu(), cu[1:] - 1)
+    reset_global_ctx()
+
+
 def test_backend_eager_batch_after_capture():
     """A decode batch larger than every captured graph runs eagerly (python/minisgl/engine/
     engine.py:194-196): 200 requests after graphs captured at batch size 8. It plans on its own

@@ -275,3 +275,49 @@ def test_prefill_head_pairs_unstaged_long_prefix_chunk_invariant():
         o, l = run(case.q[C * c: C * (c + 1)].contiguous(), cu, lens)
         assert torch.equal(o.view(torch.int16), out[C * c: C * (c + 1)].view(torch.int16)), c
         assert torch.equal(l, lse[C * c: C * (c + 1)]), c
+
+
+def test_prefill_full_bench_request_every_row():
+    """Two requests of the benchmark's batch at full size (H=64, E=2048, page 64, the batch's
+    smallest and largest prefixes), every one of their 2048 x 64 output rows and LSEs against the
+    oracle (not sampled). The whole four-request batch runs in one launch, as in the benchmark."""
+    g = torch.Generator().manual_seed(0)
+    prefixes = torch.randint(0, 8193, (4,), generator=g).tolist()
+    E, H, ps = 2048, 64, 64
+    case = make_prefill_case(H, ps, extends=[E] * 4, prefixes=prefixes, device=DEV, seed=0)
+    T = 4 * E
+    out = torch.full((T, H, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((T, H), float("nan"), dtype=torch.float32, device=DEV)
+    lib.mla_prefill(case.q, case.k_pool, case.v_pool, case.page_table, case.cu_seqlens_q, case.seq_lens_k,
+                    R.DEFAULT_SCALE, out, lse)
+    torch.cuda.synchronize()
+    kflat = case.k_pool.reshape(-1, H, 192)
+    vflat = case.v_pool.reshape(-1, H, 128)
+    for b in (min(range(4), key=lambda i: prefixes[i]), max(range(4), key=lambda i: prefixes[i])):
+        P = prefixes[b]
+        L = P + E
+        print(f"[prefill every row] request {b} prefix {P}", flush=True)
+        rows = R.token_rows(case.page_table[b].cpu(), L, ps).to(DEV)
+        k = kflat[rows].float().cpu().transpose(0, 1)
+        v = vflat[rows].float().cpu().transpose(0, 1)
+        qb = case.q[b * E : (b + 1) * E].float().cpu().transpose(0, 1)
+        mask = (torch.arange(L)[None, :] <= (P + torch.arange(E))[:, None])[None]
+        got_o = out[b * E : (b + 1) * E].float().cpu()
+        got_l = lse[b * E : (b + 1) * E].cpu()
+        for h0 in range(0, H, 16):  # the oracle's math in head chunks (bounded host memory)
+            o_ref, lse_ref = R._attend(qb[h0 : h0 + 16], k[h0 : h0 + 16], v[h0 : h0 + 16], R.DEFAULT_SCALE, mask)
+            torch.testing.assert_close(got_o[:, h0 : h0 + 16], o_ref.transpose(0, 1), **O_TOL)
+            torch.testing.assert_close(got_l[:, h0 : h0 + 16], lse_ref.transpose(0, 1), **LSE_TOL)
+
+
+def test_prefill_many_requests():
+    """130 requests in one launch (more than one 64-request chunk of the kernel's work-item scan):
+    extends 1..300 on ragged prefixes 0..900, empty-prefix and one-token requests among them."""
+    g = torch.Generator().manual_seed(12)
+    n = 130
+    extends = torch.randint(1, 301, (n,), generator=g).tolist()
+    prefixes = torch.randint(0, 901, (n,), generator=g).tolist()
+    extends[:4] = [1, 1, 300, 32]
+    prefixes[:4] = [0, 700, 0, 64]
+    case = make_prefill_case(8, 64, extends=extends, prefixes=prefixes, seed=12)
+    check_case(case)
