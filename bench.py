@@ -448,6 +448,37 @@ def _time_device(fn, stream, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
+def bench_page_size_one(args):
+    """The decode workload's batch (same lengths) in a pool of 1-token pages, the reference's default
+    page size (python/minisgl/engine/config.py:25): one-call step and split kernel alone."""
+    import torch
+
+    from minisgl_amd.benchmark.inputs import make_decode_case
+    from minisgl_amd.benchmark.layer import decode_lens
+
+    dev = torch.device("cuda:0")
+    lens = decode_lens(64, seed=0)  # the lengths _decode_workload(dev, 0) draws
+    case = make_decode_case(64, 64, 1, lens=lens, device=dev, seed=0)
+    call = _DecodeCall(case, dev)
+    stream = torch.cuda.Stream()
+    ms = _time_device(lambda: call(stream), stream, args.steps, args.warmup)
+    c = case
+
+    def split():
+        call.lib.mla_decode(c.q, c.kv_pool, c.page_table, c.seq_lens, call.plan, call.ctas, call.ws_o, call.ws_lse,
+                            (128 + 64) ** -0.5, call.out, call.lse, stream=stream, split_only=True)
+
+    split_ms = _time_device(split, stream, args.steps, args.warmup)
+    alg = case.algorithmic_bytes()
+    return {
+        "workload": "Kimi-K2-shape decode batch of the headline line (same lengths), page size 1",
+        "us_per_layer": round(ms * 1e3, 2),
+        "tb_per_s": round(alg / (ms * 1e-3) / 1e12, 4),
+        "split_kernel_us": round(split_ms * 1e3, 2),
+        "partial_slots": call.slots,
+    }
+
+
 def bench_long_context(args):
     """Long-context split-KV decode: B=8, H=64, lengths U[32768, 131072], page 64 (one layer)."""
     import torch
@@ -645,6 +676,7 @@ def main():
     if not args.no_prefill:
         res["prefill"] = bench_prefill(args)
     if not args.no_extra:
+        res["page_size_1"] = bench_page_size_one(args)
         res["long_context"] = bench_long_context(args)
         res["mixed"] = bench_mixed(args)
         res["layer"] = bench_layer(args)

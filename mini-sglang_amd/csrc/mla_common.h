@@ -118,7 +118,10 @@ hipError_t launch_prefill_gather(const void* kv, int64_t kv_row_stride, int32_t 
                                  int64_t c_row_stride, void* rope_out, int64_t rope_row_stride, int64_t out_rows,
                                  int32_t* seg_pt, int64_t seg_pt_stride, hipStream_t stream);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
-hipError_t launch_decode_ws(const DecodeParams& p, hipStream_t stream);      // heads 64, pages >= 32
+// The warp-specialized kernel: 64 heads, any power-of-two page size (under 32 tokens only while every
+// row offset of the pool fits in 32 bits).
+bool decode_ws_takes(const DecodeParams& p);
+hipError_t launch_decode_ws(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_merge(const MergeParams& p, hipStream_t stream);
 hipError_t launch_store_rows(void* cache, int64_t cache_rows, int64_t cache_stride, const void* x, int64_t x_stride,
                              const void* indices, int index_bits, int64_t rows, int64_t row_bytes,

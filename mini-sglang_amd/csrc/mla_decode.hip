@@ -428,7 +428,7 @@ hipError_t launch_decode_nw(const DecodeParams& p, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
-  if (p.heads == 64 && p.log2_ps >= 5) return launch_decode_ws(p, stream);
+  if (decode_ws_takes(p)) return launch_decode_ws(p, stream);
   if (p.heads < 1 || p.heads > 64) return hipErrorInvalidValue;  // the entry points split larger counts
   switch ((p.heads + 15) / 16) {
     case 1: return launch_decode_nw<1>(p, stream);

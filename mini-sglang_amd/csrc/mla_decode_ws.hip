@@ -53,6 +53,19 @@ struct WCursor {
   int r, t, t0, t1, q;  // request rb + r, piece [t0, t1); q < 2: query tile q, q == 2: KV tile at token t
 };
 
+// kSmall: pages of fewer than 32 tokens. A tile's rows then lie on several pages, so instead of one
+// page id per tile the DMA takes one 32-bit row offset (from the pool base) per token: score wave 0
+// loads the page-table entries of stream tile n at step n - 4, writes the tile's 32 row offsets to
+// slot n % 4 of a ring in LDS at step n - 3, and the output waves read them at step n - 2, after that
+// step's barrier, when they issue the tile. The launcher takes this path only when every row offset
+// of the pool fits in 32 bits.
+//
+// kLoop: the launch has fewer CTAs than the plan has ranges (a plan laid out for a larger grid, as a
+// captured decode step's is); CTA b then runs ranges b, b + gridDim.x, ... in turn and stops at the
+// first padding range. Without it (at most one range per compute unit) each CTA runs range blockIdx.x
+// and the body has no loop around it: the loop makes the compiler keep values across both roles'
+// step loops and spill.
+template <bool kSmall, bool kLoop>
 __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const DecodeParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kStages * kTileBytes];
   // softmax numerators of the last two scored tiles: [tile parity][head block][lane], 16 B per lane
@@ -63,25 +76,23 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
   __shared__ int s_flag[4];      // per score wave: that piece overflowed its exponent reference
   __shared__ int s_t0[kMaxCtaRequests], s_t1[kMaxCtaRequests], s_tbase[kMaxCtaRequests + 1];
   __shared__ int s_np[kMaxCtaRequests], s_slot0[kMaxCtaRequests];
-  __shared__ int s_pid[kWMaxTiles];
+  __shared__ int s_pid[kWMaxTiles];  // page id per KV tile; kSmall: the row-offset ring [4][32]
 
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool scorer = wave < 4;
   const int role = wave & 3;  // score wave: head block; output wave: value-dim quarter
-  const int g = lane >> 4;
-  const int c = lane & 15;
 
-  // The plan's ranges w, w + gridDim.x, ... of this CTA, one after another (a launch has at most one CTA
-  // per compute unit; a plan of more ranges runs as a loop, not as further rounds of CTAs).
-  for (int w = blockIdx.x; w < p.num_ctas; w += gridDim.x) {
-    if (w != (int)blockIdx.x) {  // the previous range's waves are done with the LDS tables and ring
-      wait_vmcnt<0>();
-      __syncthreads();
-    }
+  // Plan range w; false for a padding range (all later ranges are padding too).
+  auto range = [&](const int w) -> bool {
+    // the lane index from a volatile asm: what derives from it is computed per range, not hoisted
+    // out of a loop over ranges
+    int lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    const int g = lane >> 4;
+    const int c = lane & 15;
     int rb, kb, re, ke;
     sload_i32x4(p.plan + 4 * w, rb, kb, re, ke);
-    if (rb >= p.batch) break;  // the padding ranges of a plan laid out for a larger grid: all later ones too
+    if (rb >= p.batch) return false;
     const int ps_mask = (1 << p.log2_ps) - 1;
     const int row_bytes = (int)(p.kv_row_stride * 2);
     const char* kv = reinterpret_cast<const char*>(p.kv);
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     int rlast = (ke == 0 ? re - 1 : re);
     rlast = min(rlast, p.batch - 1);
     const int nreq = min(rlast - rb + 1, kMaxCtaRequests);
-    if (nreq <= 0) continue;  // uniform: an empty range
+    if (nreq <= 0) return true;  // uniform: an empty range
     for (int r = threadIdx.x; r < nreq; r += kWWaves * 64) {
       const int b = rb + r;
       const int L = p.seq_lens[b];
@@ -134,7 +145,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     }
     __syncthreads();
     const int ntiles_cta = min(s_tbase[nreq], kWMaxTiles);
-    {
+    if constexpr (!kSmall) {
       constexpr int kPer = kWMaxTiles / (kWWaves * 64);
       int pid[kPer];
 #pragma unroll
@@ -191,7 +202,8 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     for (int k = 0; k < nparts; ++k) {
       const int s = (part0 + 4 * k) * 64 + lane;
       const int t = (s * 7282) >> 19;  // s / 72 for s < 2304
-      dma_voff[k] = t * row_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4);
+      const int chunk_off = ((s - t * kRowChunks) ^ swz(t & 7)) << 4;
+      dma_voff[k] = kSmall ? (t << 16) | chunk_off : t * row_bytes + chunk_off;
     }
     int iss_kv = 0;  // KV tiles issued (index into s_pid)
     // vector-memory operations this wave issued, and the count right after its parts of stream tile n
@@ -212,6 +224,12 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
           dma16_saddr(qsrc, t * qrow_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4),
                       stage + (part0 + 4 * k) * 1024);
         }
+      } else if constexpr (kSmall) {  // each lane's token row from the offset ring (clamped rows included)
+        const int ring = (n & 3) * 32;
+#pragma unroll
+        for (int k = 0; k < nparts; ++k)
+          dma16_saddr_nt(kv, (uint32_t)s_pid[ring + (dma_voff[k] >> 16)] + (dma_voff[k] & 0xffff),
+                         stage + (part0 + 4 * k) * 1024);
       } else {
         const int pid = __builtin_amdgcn_readfirstlane(s_pid[min(iss_kv++, kWMaxTiles - 1)]);
         const char* tsrc = kv + ((int64_t)pid * (ps_mask + 1) + (cur.t & ps_mask)) * row_bytes;
@@ -251,6 +269,57 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
         iss_valid = advance(iss);
       }
     };
+    // kSmall: score wave 0's row-offset producer. la is the stream tile (index la_n) whose
+    // page-table entries are in flight; lane l (< 32) holds its token t + l, clamped to the piece.
+    WCursor la = cs;
+    int la_n = 0, la_tok = 0, la_page = 0;
+    bool la_valid = false, la_kv = false;
+    auto la_load = [&]() {
+      la_kv = la_valid && la.q == 2;
+      if (la_kv) {
+        la_tok = min(la.t + (lane & 31), la.t1 - 1);
+        la_page = p.page_table[(int64_t)(rb + la.r) * p.pt_stride + (la_tok >> p.log2_ps)];
+      }
+    };
+    auto la_store = [&]() {  // waits for la_page (this wave issues no other vector-memory loads)
+      if (la_kv && lane < 32) {
+        const uint32_t page = (uint32_t)min(max(la_page, 0), p.num_pages - 1);
+        s_pid[(la_n & 3) * 32 + lane] = (int)(((page << p.log2_ps) | (uint32_t)(la_tok & ps_mask)) * (uint32_t)row_bytes);
+      }
+    };
+    auto la_step = [&]() {  // store the in-flight tile's offsets, then load the next tile's entries
+      la_store();
+      if (la_valid) la_valid = advance(la);
+      ++la_n;
+      la_load();
+    };
+    auto seed = [&](const WCursor& from, int n0) {  // offsets of tiles n0 .. n0 + 2; n0 + 3 in flight
+      la = from;
+      la_valid = true;
+      int tok[3], pg[3];
+      bool kv3[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {  // the three tiles' page-table loads back to back
+        kv3[i] = la_valid && la.q == 2;
+        tok[i] = min(la.t + (lane & 31), la.t1 - 1);
+        pg[i] = kv3[i] ? p.page_table[(int64_t)(rb + la.r) * p.pt_stride + (tok[i] >> p.log2_ps)] : 0;
+        if (la_valid) la_valid = advance(la);
+      }
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        if (kv3[i] && lane < 32) {
+          const uint32_t page = (uint32_t)min(max(pg[i], 0), p.num_pages - 1);
+          s_pid[((n0 + i) & 3) * 32 + lane] =
+              (int)(((page << p.log2_ps) | (uint32_t)(tok[i] & ps_mask)) * (uint32_t)row_bytes);
+        }
+      }
+      la_n = n0 + 3;
+      la_load();
+    };
+    if constexpr (kSmall) {  // every wave: the first tiles' offsets before the first DMA
+      if constexpr (kScore) if (role == 0) seed(cs, 0);
+      barrier_lds();
+    }
     prologue();
 
     // score-wave state: queries of head blocks 2 hg, 2 hg + 1; per head block (lane: head c of it)
@@ -314,6 +383,10 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
         s_valid = true;
         prev_kv = false;
         ops = 0;
+        if constexpr (kSmall) {  // the rewound tiles' offsets again (their ring slots were reused)
+          if constexpr (kScore) if (role == 0) seed(piece_cur, piece_j);
+          barrier_lds();
+        }
         prologue();
         continue;
       }
@@ -530,6 +603,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
         issue(iss, n_issued++);
         iss_valid = advance(iss);
       }
+      if constexpr (kSmall && kScore) if (role == 0) la_step();  // tile j + 3's offsets, tile j + 4 in flight
       // ---- advance: tile j becomes the previous tile
       prev_kv = cur_kv;
       prev_end = cur_end;
@@ -545,14 +619,43 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     };
     if (scorer) run(std::true_type{});
     else run(std::false_type{});
+    return true;
+  };
+
+  if constexpr (kLoop) {
+    for (int w = blockIdx.x; w < p.num_ctas; w += gridDim.x) {
+      if (w != (int)blockIdx.x) {  // the previous range's waves are done with the LDS tables and ring
+        wait_vmcnt<0>();
+        __syncthreads();
+      }
+      if (!range(w)) break;
+    }
+  } else {
+    range(blockIdx.x);
   }
 }
 
 }  // namespace
 
+bool decode_ws_takes(const DecodeParams& p) {
+  if (p.heads != 64) return false;
+  if (p.log2_ps >= 5) return true;
+  // pages under 32 tokens: every row offset from the pool base must fit in 32 bits
+  return ((int64_t)p.num_pages << p.log2_ps) * p.kv_row_stride * 2 <= (int64_t)UINT32_MAX;
+}
+
+template <bool kSmall>
+static void launch_ws(const DecodeParams& p, hipStream_t stream) {
+  const int cus = current_device_cus();
+  if (p.num_ctas <= cus)
+    hipLaunchKernelGGL((mla_decode_ws_kernel<kSmall, false>), dim3(p.num_ctas), dim3(kWWaves * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((mla_decode_ws_kernel<kSmall, true>), dim3(cus), dim3(kWWaves * 64), 0, stream, p);
+}
+
 hipError_t launch_decode_ws(const DecodeParams& p, hipStream_t stream) {
-  const int grid = p.num_ctas < current_device_cus() ? p.num_ctas : current_device_cus();
-  hipLaunchKernelGGL(mla_decode_ws_kernel, dim3(grid), dim3(kWWaves * 64), 0, stream, p);
+  if (p.log2_ps >= 5) launch_ws<false>(p, stream);
+  else launch_ws<true>(p, stream);
   return hipGetLastError();
 }
 

@@ -437,3 +437,68 @@ def test_decode_long_pieces_small_pages(heads, ps, num_ctas):
     longest = max(t1 - t0 for *_, t0, t1 in plan_pieces(plan_np, num_ctas, lens))
     assert num_ctas > 1 or longest > 1024 * ps, "one CTA takes the long request whole"
     check_case(case, num_ctas)
+
+
+@pytest.mark.parametrize("ps,num_ctas", [(4, 256), (8, 5), (1, 9)])
+def test_decode_64_heads_small_pages(ps, num_ctas):
+    """64 heads with pages under 32 tokens (the streaming kernel with per-token row offsets): tiles
+    that straddle pages, pieces shorter than a tile, lengths that are not multiples of 32."""
+    case = make_decode_case(9, 64, ps, lens=[1, 33, 64, 96, 130, 255, 1000, 2049, 31], seed=100 + ps)
+    check_case(case, num_ctas)
+
+
+@pytest.mark.parametrize("ps", [1, 8])
+def test_decode_large_logits_small_pages(ps):
+    """The exact-max rerun of a piece with pages under 32 tokens: the rerun rewinds the stream, so
+    the rewound tiles' row offsets are produced again."""
+    case = make_decode_case(2, 64, ps, lens=[900, 2000], seed=19)
+    ramp = torch.linspace(0, 90.0, case.kv_pool.shape[0] * ps).view(-1, ps, 1)
+    kv = case.kv_pool.float()
+    kv[..., 512:513] = ramp
+    case.kv_pool = kv.to(torch.bfloat16)
+    case.q[..., 512] = 20.0
+    check_case(case, 8)
+
+
+def test_decode_kimi_k2_page_size_one_more_ranges_than_compute_units():
+    """The benchmark's batch at page size 1 (the reference's default), planned over 512 ranges: the
+    streaming kernel with per-token row offsets, each CTA running two ranges in turn."""
+    case = make_decode_case(64, 64, 1, len_range=(1024, 8192), device=DEV, seed=6)
+    out, lse, slots = run_decode(case.q, case.kv_pool, case.page_table, case.seq_lens, case.lens, 1, 512)
+    assert slots > 2 * 256
+    o_ref, lse_ref = R.mla_decode(case.q.cpu(), case.kv_pool.cpu(), case.page_table.cpu(), case.lens)
+    torch.testing.assert_close(out, o_ref, **O_TOL)
+    torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
+
+
+def test_decode_small_pages_pool_beyond_32_bit_offsets():
+    """A page-size-1 pool of more than 4 GiB: row offsets from the pool base no longer fit in 32
+    bits, so 64 heads take the general kernel (64-bit row addresses); rows at the far end of the pool
+    are read correctly."""
+    pages = (1 << 32) // 1152 + 4096  # 4.0 GiB + 4.5 MiB of rows
+    lens = [300, 77, 1500]
+    g = torch.Generator().manual_seed(31)
+    pool = torch.empty((pages, 1, 576), dtype=torch.bfloat16, device=DEV)
+    pt = torch.zeros((3, 1500), dtype=torch.int32)
+    used = torch.cat([torch.arange(pages - 2000, pages), torch.arange(0, 2000)])[torch.randperm(4000, generator=g)]
+    off = 0
+    for b, L in enumerate(lens):
+        pt[b, :L] = used[off : off + L].to(torch.int32)
+        off += L
+    rows = torch.randn((4000, 1, 576), generator=g).to(torch.bfloat16)
+    pool[pages - 2000 :] = rows[:2000].to(DEV)
+    pool[:2000] = rows[2000:].to(DEV)
+    q = torch.randn((3, 64, 576), generator=g).to(torch.bfloat16)
+    small = torch.cat([rows[2000:], rows[:2000]])  # pool pages [0, 2000) then [pages - 2000, pages)
+    # the oracle over the same rows, renumbered into a 4000-page pool
+    remap = torch.full((pages,), -1, dtype=torch.int64)
+    remap[:2000] = torch.arange(2000)
+    remap[pages - 2000 :] = torch.arange(2000, 4000)
+    pt_small = remap[pt.long()].to(torch.int32)
+    pt_small[pt_small < 0] = 0
+    o_ref, lse_ref = R.mla_decode(q, small, pt_small, lens)
+    out, lse, _ = run_decode(q.to(DEV), pool, pt.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV), lens,
+                             1, 256)
+    del pool
+    torch.testing.assert_close(out, o_ref, **O_TOL)
+    torch.testing.assert_close(lse, lse_ref, **LSE_TOL)
