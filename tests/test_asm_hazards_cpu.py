@@ -170,11 +170,13 @@ class Function:
 
 
 def functions(asm: str) -> List[Function]:
-    """The code symbols of ``asm`` (kernels and device functions), each up to its .Lfunc_end."""
+    """The code symbols of ``asm`` (``.type <name>,@function``: kernels and device functions), each
+    up to its .Lfunc_end."""
+    code = set(re.findall(r"\.type\s+([\w.$]+),@function", asm))
     out, name, body = [], None, []
     for line in asm.splitlines():
         m = re.match(r"^([A-Za-z_][\w.$]*):(\s|;|$)", line)
-        if m and not line.startswith(".") and not m.group(1).startswith(("amdhsa", "__hip_cuid")):
+        if m and m.group(1) in code:
             if name is not None:
                 out.append(Function(name, body))
             name, body = m.group(1), []
@@ -223,6 +225,7 @@ def find_hazards(asm: str):
 
 def test_checker_catches_a_readfirstlane_feeding_a_dma():
     asm = """
+        .type k,@function
 k:
         v_readfirstlane_b32 s1, v3
         v_readfirstlane_b32 s0, v2
@@ -245,6 +248,7 @@ def test_checker_follows_loop_back_edges_and_branches():
     lane mask and a carry-out feed DMAs across a branch; the same code with enough wait states on
     every path is clean."""
     bad = """
+        .type k,@function
 k:
         s_mov_b32 s4, 0
 .LBB0_1:
@@ -280,6 +284,7 @@ k:
 
 def test_checker_m0_across_a_branch():
     asm = """
+        .type k,@function
 k:
         s_cbranch_execz .LBB0_2
         s_mov_b32 m0, s3
@@ -295,9 +300,11 @@ k:
 @pytest.mark.skipif(shutil.which(HIPCC) is None and not os.path.exists(HIPCC), reason="hipcc not available")
 @pytest.mark.parametrize("src", [os.path.basename(s) for s in SOURCES])
 def test_no_dma_hazards(src, tmp_path):
-    asm = _device_asm(os.path.join(build.CSRC, src), str(tmp_path))
-    fns = functions(asm)
-    assert fns and all(len(f.blocks) > 0 for f in fns)
+    path = os.path.join(build.CSRC, src)
+    asm = _device_asm(path, str(tmp_path))
+    with open(path) as f:
+        has_kernels = "__global__" in f.read()
+    assert bool(functions(asm)) == has_kernels, "kernel symbols not found in the device assembly"
     sgpr, m0 = find_hazards(asm)
     assert not sgpr, f"VALU-written SGPR read by a memory instruction too early: {sgpr[:3]}"
     assert not m0, f"M0 written right before an LDS DMA: {m0[:3]}"
