@@ -115,6 +115,28 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     rlast = min(rlast, p.batch - 1);
     const int nreq = min(rlast - rb + 1, kMaxCtaRequests);
     if (nreq <= 0) return true;  // uniform: an empty range
+    // The first piece is request rb's in all but rare cases (rb's part of the range is empty only for
+    // an empty request): the output waves load its two query tiles into ring stages 0 and 1 now, so
+    // that they land while the range is staged (the staging's barriers wait on LDS only). If the
+    // first piece turns out to be another request's, the stream issues its query tiles into the same
+    // stages after these loads, and loads of one wave complete in order.
+    constexpr int kEarlyQueryDma = 2 * kWOutParts;
+    if (!scorer) {
+      const int qrow_bytes = (int)(p.q_stride_h * 2);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const char* qsrc = reinterpret_cast<const char*>(p.q) +
+                           ((int64_t)rb * p.q_stride_b + (int64_t)(32 * qt) * p.q_stride_h) * 2;
+#pragma unroll
+        for (int k = 0; k < kWOutParts; ++k) {
+          const int part = 4 * kWScoreParts + role + 4 * k;
+          const int s = part * 64 + lane;
+          const int t = (s * 7282) >> 19;  // s / 72
+          dma16_saddr(qsrc, t * qrow_bytes + (((s - t * kRowChunks) ^ swz(t & 7)) << 4),
+                      lds_ring + qt * kTileBytes + part * 1024);
+        }
+      }
+    }
     for (int r = threadIdx.x; r < nreq; r += kWWaves * 64) {
       const int b = rb + r;
       const int L = p.seq_lens[b];
@@ -127,7 +149,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
       s_np[r] = p.plan[4 * p.num_ctas + 3 * b + 1];
       s_slot0[r] = p.plan[4 * p.num_ctas + 3 * b + 2] - first;
     }
-    __syncthreads();
+    barrier_lds();
     if (wave == 0) {  // exclusive prefix of tile counts (64-wide scans)
       int carry = 0;
       for (int c0 = 0; c0 < nreq; c0 += 64) {
@@ -143,7 +165,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
       }
       if (lane == 0) s_tbase[0] = 0;
     }
-    __syncthreads();
+    barrier_lds();
     const int ntiles_cta = min(s_tbase[nreq], kWMaxTiles);
     if constexpr (!kSmall) {
       constexpr int kPer = kWMaxTiles / (kWWaves * 64);
@@ -169,7 +191,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
         if (k < ntiles_cta) s_pid[k] = min(max(pid[u], 0), p.num_pages - 1);
       }
     }
-    __syncthreads();
+    barrier_lds();
 
     // ---- stream cursors over (request, tile); all values wave-uniform
     auto seek = [&](WCursor& cur, int r) -> bool {  // first non-empty piece at or after request rb + r
@@ -208,7 +230,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     int iss_kv = 0;  // KV tiles issued (index into s_pid)
     // vector-memory operations this wave issued, and the count right after its parts of stream tile n
     // (kept for n % 4): tile n has landed once at most (ops - mark) operations are outstanding
-    int ops = 0, mark0 = 0, mark1 = 0, mark2 = 0, mark3 = 0;
+    int ops = kScore ? 0 : kEarlyQueryDma, mark0 = kScore ? 0 : kWOutParts, mark1 = ops, mark2 = 0, mark3 = 0;
     auto issue = [&](const WCursor& cur, int n) {  // this wave's DMA parts of stream tile n (at cur)
       const uint32_t stage = lds_ring + (n % kStages) * kTileBytes;
       if (cur.q < 2) {  // query rows 32q .. +32 of request rb + r
@@ -258,13 +280,27 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
     };
 
     WCursor cs;  // the tile scored at this step
-    if (!seek(cs, 0)) return;  // uniform: every piece of the range is empty (no barrier follows)
+    if (!seek(cs, 0)) {  // uniform: every piece of the range is empty (no barrier follows)
+      wait_vmcnt<0>();   // the early query loads land before the CTA can end
+      return;
+    }
     WCursor iss = cs;
     int n_issued = 0;
     bool iss_valid = true;
-    auto prologue = [&]() {
+    if constexpr (nparts > 0) {
+      if (cs.r == 0) {  // the early query loads are stream tiles 0 and 1 (a piece starts at q = 0)
+        for (int s = 0; s < 2 && iss_valid; ++s) {
+          ++n_issued;
+          iss_valid = advance(iss);
+        }
+      } else {  // request rb is empty: its query loads land before the stream reuses their stages
+        wait_vmcnt<0>();
+        ops = mark0 = mark1 = 0;
+      }
+    }
+    auto prologue = [&](const int from) {
       if constexpr (nparts == 0) return;  // a role without DMA parts keeps no issue cursor
-      for (int s = 0; s < kWAhead && iss_valid; ++s) {
+      for (int s = from; s < kWAhead && iss_valid; ++s) {
         issue(iss, n_issued++);
         iss_valid = advance(iss);
       }
@@ -320,7 +356,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
       if constexpr (kScore) if (role == 0) seed(cs, 0);
       barrier_lds();
     }
-    prologue();
+    prologue(n_issued);
 
     // score-wave state: queries of head blocks 2 hg, 2 hg + 1; per head block (lane: head c of it)
     // the piece's reference, max and this half's row sum
@@ -387,7 +423,7 @@ __global__ __launch_bounds__(kWWaves * 64, 1) void mla_decode_ws_kernel(const De
           if constexpr (kScore) if (role == 0) seed(piece_cur, piece_j);
           barrier_lds();
         }
-        prologue();
+        prologue(0);
         continue;
       }
       if (prev_kv && prev_end) attempt = 0;

@@ -85,6 +85,24 @@ def valu_sgpr_dests(line: str) -> Set[str]:
     return set()
 
 
+# scalar-ALU and scalar-load opcodes whose first operand is their destination
+_SALU_DST = re.compile(r"^s_(mov|movk|cmov|cmovk|cselect|add|addc|addk|sub|subb|mul|mulk|mul_hi|lshl|lshr|ashr|"
+                       r"lshl[1-4]_add|and|or|xor|andn2|orn2|nand|nor|xnor|not|bfe|bfm|min|max|abs|absdiff|brev|"
+                       r"ff0|ff1|flbit|bcnt0|bcnt1|sext|pack|getpc|load|buffer_load)(_|$)")
+
+
+def sgpr_dests(line: str) -> Set[str]:
+    """Scalar registers any instruction writes, as far as the checker needs to know: vector-ALU
+    scalar destinations and the destinations of scalar-ALU ops and scalar loads."""
+    op = line.split()[0]
+    if op.startswith("v_"):
+        return valu_sgpr_dests(line)
+    ops = _operands(line)
+    if ops and _SALU_DST.match(op):
+        return _sgprs(ops[0])
+    return set()
+
+
 def _is_vmem(op: str) -> bool:
     return op.startswith(("global_", "buffer_", "flat_", "scratch_"))
 
@@ -146,26 +164,30 @@ class Function:
 
     def writers_within(self, block: int, index: int, regs: Set[str], budget: int, pick) -> List[str]:
         """Instructions on any path into (block, index) that ``pick(line) & regs`` and lie fewer
-        than ``budget`` wait states before it."""
+        than ``budget`` wait states before it, counting only the last write of each register on
+        the path (a later write by any instruction, scalar ALU included, hides an earlier one)."""
         found: List[str] = []
-        seen: Set[Tuple[int, int]] = set()
+        seen: Set[Tuple[int, int, frozenset]] = set()
 
-        def walk(b: int, i: int, left: int):
-            if (b, left) in seen:
+        def walk(b: int, i: int, left: int, live: frozenset):
+            if (b, left, live) in seen:
                 return
-            seen.add((b, left))
+            seen.add((b, left, live))
             ins = self.blocks[b]
             for j in range(i - 1, -1, -1):
-                if pick(ins[j]) & regs:
+                if pick(ins[j]) & live:
                     found.append(ins[j])
+                    return
+                live = live - sgpr_dests(ins[j])
+                if not live:
                     return
                 left -= _waits_of(ins[j])
                 if left <= 0:
                     return
             for p in self.preds[b]:
-                walk(p, len(self.blocks[p]), left)
+                walk(p, len(self.blocks[p]), left, live)
 
-        walk(block, index, budget)
+        walk(block, index, budget, frozenset(regs))
         return found
 
 
@@ -280,6 +302,29 @@ k:
         "s_cbranch_vccz .LBB0_3\n        s_nop 1", "s_nop 4\n        s_cbranch_vccz .LBB0_3\n        s_nop 1").replace(
         "v_add_co_u32_e64 v5, s[10:11], v6, v7", "v_add_co_u32_e64 v5, s[10:11], v6, v7\n        s_nop 4")
     assert find_hazards(good) == ([], [])
+
+
+def test_checker_counts_the_last_write_only():
+    """A spilled address restored with readlanes and then rebuilt by scalar adds is read by the DMA
+    from the scalar writes: no hazard. Rebuilding only its low half leaves the readlane of the high
+    half as the last write: a hazard."""
+    asm = """
+        .type k,@function
+k:
+        v_readlane_b32 s4, v239, 10
+        s_add_u32 s4, s4, s8
+        v_readlane_b32 s5, v239, 11
+        s_addc_u32 s5, s5, s3
+        s_mov_b32 m0, s3
+        s_nop 0
+        global_load_lds_dwordx4 v4, s[4:5]
+        s_endpgm
+.Lfunc_end0:
+    """
+    assert find_hazards(asm) == ([], [])
+    half = asm.replace("s_addc_u32 s5, s5, s3", "s_nop 0")
+    sgpr, m0 = find_hazards(half)
+    assert len(sgpr) == 1 and "v_readlane_b32 s5" in sgpr[0][1] and not m0
 
 
 def test_checker_m0_across_a_branch():
